@@ -1,0 +1,198 @@
+/*
+ * specgrove_hip.h -- C ABI of libspecgrove_hip.so, the MI355X (gfx950) kernels
+ * of SpecGrove's packed target-verification path.
+ *
+ * Conventions
+ *   - Every pointer named *_dev is a device pointer owned by the caller; the
+ *     library never allocates or frees device memory and never synchronises
+ *     the device.  Work is enqueued on the given stream only.
+ *   - Host pointers (named *_host) are read before the call returns.
+ *   - Return 0 on success or a negative SG_E* code; sg_last_error() returns a
+ *     thread-local message for the last failure on the calling thread.
+ *   - bf16 tensors are passed as void* (raw 16-bit storage); the head
+ *     dimension is contiguous, the other strides are given in elements.
+ *
+ * Reference interfaces replaced (paths relative to the reference snapshot;
+ * CTBD = code/natural/src/gbv_experiments/continuous_tree_block_decode.py,
+ * FTS = code/natural/src/gbv_experiments/fused_tree_sampling.py,
+ * SMP = code/natural/src/gbv_experiments/sampling.py).
+ */
+#ifndef SPECGROVE_HIP_H
+#define SPECGROVE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SG_ABI_VERSION 1
+
+#define SG_OK 0
+#define SG_EINVAL (-1)  /* shape or contract violation (Python: ValueError) */
+#define SG_ERANGE (-2)  /* KV capacity exhausted (Python: RuntimeError) */
+#define SG_EHIP (-3)    /* HIP launch/runtime error (Python: RuntimeError) */
+
+typedef struct ihipStream_t* sg_stream_t; /* == hipStream_t */
+
+/* ABI version (SG_ABI_VERSION).  No reference counterpart. */
+int sg_abi_version(void);
+
+/* Message of the last error on this thread ("" if none).  Plays the role of
+ * TORCH_CHECK's RuntimeError text in FTS:158-174. */
+const char* sg_last_error(void);
+
+/* ------------------------------------------------------------------------
+ * (A) Request-isolated, tree-ancestor-masked GQA attention.
+ *
+ * Replaces the packed target wave's attention: _pack_cache_sequence
+ * (CTBD:313-361) + the dense mask of _packed_block_inputs (CTBD:500-546) +
+ * transformers' repeat_kv + F.scaled_dot_product_attention (called through
+ * Engine.target_hidden_forward, code/natural/src/gbv_experiments/engine.py:499-517,
+ * attention plug point engine.py:278-281).  Row q_i+k of request i attends to
+ * the request's own cached prefix and to the tree rows that are ancestors of k
+ * (or k itself), exactly the visible set of CTBD:535-545 / tree.py:19-26.
+ * ---------------------------------------------------------------------- */
+typedef struct SgTreeAttnArgs {
+  int32_t num_requests;   /* n */
+  int32_t num_rows;       /* R = row_offset[n] */
+  int32_t num_q_heads;    /* Hq */
+  int32_t num_kv_heads;   /* Hkv; Hq % Hkv == 0, Hq/Hkv <= 8 */
+  int32_t head_dim;       /* D: 64 or 128 */
+  float scale;            /* softmax scale, usually D^-0.5 */
+  /* queries [R, Hq, D] bf16 */
+  const void* q_dev;
+  int64_t q_row_stride, q_head_stride;
+  /* cached prefix K/V: element (head g, token t) at base + g*head_stride + t*token_stride */
+  const void* k_cache_dev;
+  const void* v_cache_dev;
+  int64_t cache_head_stride, cache_token_stride;
+  /* this wave's tree-row K/V [R, Hkv, D] bf16 (not yet in the cache) */
+  const void* k_tree_dev;
+  const void* v_tree_dev;
+  int64_t tree_row_stride, tree_head_stride;
+  /* request metadata (device, int32) */
+  const int32_t* row_offset_dev;   /* [n+1] */
+  const int64_t* prefix_start_dev; /* [n] first cache token of request i (slot*capacity) */
+  const int32_t* prefix_len_dev;   /* [n] cached prefix length L_i */
+  const int32_t* parent_dev;       /* [R] request-local parent row, -1 for the root */
+  /* output [R, Hq, D] bf16 */
+  void* out_dev;
+  int64_t out_row_stride, out_head_stride;
+  /* work plan from sg_tree_attn_plan (device copy) and its scratch */
+  const void* plan_dev;
+  int32_t plan_units;    /* work units (first kernel's grid) */
+  int32_t plan_merges;   /* split-K merge groups (second kernel's grid) */
+  void* workspace_dev;
+  size_t workspace_bytes;
+} SgTreeAttnArgs;
+
+/* Host-side planner.  From host copies of row_offset [n+1] and prefix_len [n]
+ * it writes the work list (plan_capacity_bytes of host memory) and reports its
+ * size, unit count and the scratch bytes sg_tree_attn_fwd needs.  Replaces the
+ * host index lists the reference builds per wave (CTBD:327-350, :513-545).
+ * target_units_hint <= 0 lets the planner size splits for 256 CUs. */
+int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset_host,
+                      const int32_t* prefix_len_host, int32_t num_q_heads,
+                      int32_t num_kv_heads, int32_t head_dim,
+                      int32_t target_units_hint, void* plan_host,
+                      size_t plan_capacity_bytes, size_t* plan_bytes,
+                      int32_t* plan_units, int32_t* plan_merges,
+                      size_t* workspace_bytes);
+
+/* Enqueue the attention of one layer. */
+int sg_tree_attn_fwd(const SgTreeAttnArgs* args, sg_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * (B) Accepted-path KV commit.
+ *
+ * Replaces _PersistentRequestCachePool.append_packed_sequence (CTBD:215-261)
+ * with the keep rule keep_i = [0] + accepted local nodes (CTBD:2108-2109):
+ *   cache[l][g, prefix_start_i + len_i + t] = tree[l][row_offset_i + keep_i[t], g]
+ * for every layer l, kv head g and t < keep_len_i.  If len_i + keep_len_i
+ * exceeds capacity the request is not written and *status_dev is set to
+ * SG_ERANGE (the reference raises "Persistent request KV capacity exhausted",
+ * CTBD:235-236); callers check capacity on the host first.
+ * ---------------------------------------------------------------------- */
+typedef struct SgKvCommitArgs {
+  int32_t num_layers;
+  int32_t num_requests;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  /* per-layer cache bases (device arrays of num_layers device pointers) */
+  void* const* k_cache_layers_dev;
+  void* const* v_cache_layers_dev;
+  int64_t cache_head_stride, cache_token_stride;
+  /* per-layer tree-row K/V bases [R, Hkv, D] (device arrays of pointers) */
+  const void* const* k_tree_layers_dev;
+  const void* const* v_tree_layers_dev;
+  int64_t tree_row_stride, tree_head_stride;
+  const int32_t* row_offset_dev;   /* [n+1] packed row range of request i */
+  const int32_t* keep_rows_dev;    /* [n, keep_stride] local rows, ascending path order */
+  int32_t keep_stride;
+  const int32_t* keep_len_dev;     /* [n] */
+  const int64_t* prefix_start_dev; /* [n] slot_i * capacity */
+  int32_t* lengths_dev;            /* [n] cached length of request i; advanced in place */
+  int32_t capacity;
+  int32_t* status_dev;             /* optional [1]; SG_ERANGE on overflow */
+} SgKvCommitArgs;
+
+int sg_kv_commit(const SgKvCommitArgs* args, sg_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * (C) Temperature-1 tree rejection sampling over a packed wave.
+ *
+ * Replaces the fp32 softmax + ancestral verification of the formal path
+ * (probabilities SMP:29-36 via CTBD:1821-1824, tree_verify_ancestral_batched
+ * SMP:903-950) and the inline CUDA samplers (FTS:103-2058, sparse-exit layout
+ * FTS:683-824): per request, starting at the root row, the route uniform
+ * u[2d] accepts the first child (ascending node order) whose cumulative
+ * target mass exceeds u[2d]*Z; otherwise u[2d+1] draws the bonus token from
+ * the complement of the children (full row at a leaf), fallback = largest
+ * non-child token (FTS:804-818).  fp32 throughout with a fixed reduction
+ * order, so results are bit-reproducible.
+ * ---------------------------------------------------------------------- */
+typedef struct SgTreeSampleArgs {
+  int32_t num_requests;
+  int32_t num_rows;
+  int32_t vocab;              /* V <= 524288 */
+  int32_t max_depth;          /* accept_nodes slots per request */
+  const float* logits_dev;    /* [R, logits_row_stride] fp32 target logits (T = 1) */
+  int64_t logits_row_stride;
+  const int32_t* row_offset_dev; /* [n+1] */
+  const int32_t* parent_dev;     /* [R] local parent, -1 for roots */
+  const int32_t* token_dev;      /* [R] draft token of each node (root entry unused) */
+  const float* uniforms_dev;     /* [n, uniform_stride] fp32 in [0,1) */
+  int32_t uniform_stride;        /* >= 2*(max_depth+1) */
+  float* row_max_dev;            /* [R] scratch/output: row max */
+  float* row_sum_dev;            /* [R] scratch/output: sum of exp(x - max) */
+  int32_t* accept_nodes_dev;     /* [n, max_depth] local node ids, -1 padded */
+  int32_t* accept_len_dev;       /* [n] */
+  int32_t* bonus_dev;            /* [n] */
+  int32_t* keep_rows_dev;        /* optional [n, max_depth+1]: [0] + nodes, -1 padded */
+  int32_t* status_dev;           /* optional [1]: SG_EINVAL if a walk broke the contract */
+} SgTreeSampleArgs;
+
+/* Row statistics of all packed rows followed by the per-request walk. */
+int sg_tree_sample(const SgTreeSampleArgs* args, sg_stream_t stream);
+
+/* Row statistics only (max and sum of exp of each logits row). */
+int sg_row_stats(const float* logits_dev, int64_t row_stride, int32_t vocab,
+                 int32_t num_rows, float* row_max_dev, float* row_sum_dev,
+                 sg_stream_t stream);
+
+/* sizeof() of the argument structs as compiled into the library, for binding
+ * checks: which = 0 SgTreeAttnArgs, 1 SgKvCommitArgs, 2 SgTreeSampleArgs.
+ * Returns -1 for an unknown index.  No reference counterpart. */
+int64_t sg_abi_struct_size(int32_t which);
+
+/* Test hook: E(x) of the sampler's exp for count values (device arrays). */
+int sg_exp_probe(const float* x_dev, float* out_dev, int64_t count,
+                 sg_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPECGROVE_HIP_H */

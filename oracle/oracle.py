@@ -1,0 +1,357 @@
+"""CPU oracle for the packed tree-verification path.
+
+TEST INFRASTRUCTURE ONLY.  Only tests/, ``__graft_entry__.smoke()`` and the
+CPU-baseline leg of ``bench.py`` may import this module; the product package
+(``specgrove_amd``) never does.  Every function restates the reference's
+semantics on the CPU and cites the reference file it follows (paths relative
+to the reference snapshot, ``CTBD`` = code/natural/src/gbv_experiments/
+continuous_tree_block_decode.py).
+
+Parts:
+  * packing  -- ancestor visibility (tree.py:19-26) and the dense additive
+                packed mask / ids / positions (CTBD:500-546);
+  * attention -- textbook masked softmax attention in fp32 on bf16-valued
+                inputs, GQA head h -> kv head h // (Hq/Hkv) as transformers'
+                repeat_kv (dense packed mode = the reference wave; per-request
+                mode = the same math restricted to a request's own keys);
+  * commit   -- the persistent-arena scatter of CTBD:215-261 with the keep rule
+                of CTBD:2108-2109;
+  * sampling -- ctypes binding of sg_oracle.c (explicit-uniform tree rejection
+                sampler, law of sampling.py:903-950) plus the ancestral walk of
+                sampling.py:937-950 on pre-drawn posterior tokens.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from pathlib import Path
+from typing import Sequence
+
+import numpy as np
+
+_HERE = Path(__file__).resolve().parent
+_LIB_PATH = _HERE / "libsg_oracle.so"
+_lib = None
+
+
+def build_oracle_library() -> Path:
+    """Compile sg_oracle.c with the committed Makefile (gcc only)."""
+    import subprocess
+    subprocess.run(["make", "-s", "-C", str(_HERE)], check=True)
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not _LIB_PATH.exists():
+            build_oracle_library()
+        handle = ctypes.CDLL(str(_LIB_PATH))
+        f32p = ctypes.POINTER(ctypes.c_float)
+        i32p = ctypes.POINTER(ctypes.c_int32)
+        handle.sgo_exp.restype = ctypes.c_float
+        handle.sgo_exp.argtypes = [ctypes.c_float]
+        handle.sgo_exp_array.restype = None
+        handle.sgo_exp_array.argtypes = [f32p, f32p, ctypes.c_int64]
+        handle.sgo_row_stats.restype = None
+        handle.sgo_row_stats.argtypes = [f32p, ctypes.c_int64, f32p, f32p]
+        handle.sgo_complement_draw.restype = ctypes.c_int32
+        handle.sgo_complement_draw.argtypes = [
+            f32p, ctypes.c_int64, ctypes.c_float, i32p, ctypes.c_int,
+            ctypes.c_float, f32p,
+        ]
+        handle.sgo_tree_sample.restype = ctypes.c_int
+        handle.sgo_tree_sample.argtypes = [
+            f32p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, i32p, i32p,
+            i32p, f32p, ctypes.c_int32, ctypes.c_int32, i32p, i32p, i32p,
+            f32p, f32p,
+        ]
+        _lib = handle
+    return _lib
+
+
+def _f32p(array: np.ndarray):
+    return array.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+def _i32p(array: np.ndarray):
+    return array.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+
+
+# --------------------------------------------------------------------------
+# Sampling (sg_oracle.c)
+# --------------------------------------------------------------------------
+
+def exp_f32(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().sgo_exp_array(_f32p(x), _f32p(out), x.size)
+    return out
+
+
+def row_stats(row: np.ndarray) -> tuple[float, float]:
+    row = np.ascontiguousarray(row, dtype=np.float32)
+    m = np.zeros(1, np.float32)
+    z = np.zeros(1, np.float32)
+    lib().sgo_row_stats(_f32p(row), row.size, _f32p(m), _f32p(z))
+    return float(m[0]), float(z[0])
+
+
+def complement_draw(row: np.ndarray, m: float, child_tokens: Sequence[int],
+                    u: float) -> tuple[int, float]:
+    row = np.ascontiguousarray(row, dtype=np.float32)
+    children = np.ascontiguousarray(np.asarray(child_tokens, np.int32))
+    total = np.zeros(1, np.float32)
+    token = lib().sgo_complement_draw(
+        _f32p(row), row.size, np.float32(m), _i32p(children), children.size,
+        np.float32(u), _f32p(total),
+    )
+    return int(token), float(total[0])
+
+
+def tree_sample(logits: np.ndarray, row_offset: np.ndarray, parent: np.ndarray,
+                token: np.ndarray, uniforms: np.ndarray, max_depth: int):
+    """Oracle for the packed sampler.
+
+    ``logits`` [rows, V] fp32, ``row_offset`` [n+1], ``parent``/``token``
+    [rows] int32 (request-local parent, -1 root), ``uniforms`` [n, U] fp32.
+    Returns (accept_nodes [n, max_depth], accept_len [n], bonus [n],
+    row_m [rows], row_z [rows]).
+    """
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    row_offset = np.ascontiguousarray(row_offset, dtype=np.int32)
+    parent = np.ascontiguousarray(parent, dtype=np.int32)
+    token = np.ascontiguousarray(token, dtype=np.int32)
+    uniforms = np.ascontiguousarray(uniforms, dtype=np.float32)
+    n = row_offset.size - 1
+    rows = int(row_offset[-1])
+    if logits.ndim != 2 or logits.shape[0] < rows:
+        raise ValueError("logits do not cover the packed rows")
+    depth_slots = max(int(max_depth), 1)
+    nodes = np.full((n, depth_slots), -1, np.int32)
+    length = np.zeros(n, np.int32)
+    bonus = np.zeros(n, np.int32)
+    row_m = np.zeros(rows, np.float32)
+    row_z = np.zeros(rows, np.float32)
+    status = lib().sgo_tree_sample(
+        _f32p(logits), logits.shape[1], logits.shape[1], n, _i32p(row_offset),
+        _i32p(parent), _i32p(token), _f32p(uniforms), uniforms.shape[1],
+        int(max_depth), _i32p(nodes), _i32p(length), _i32p(bonus),
+        _f32p(row_m), _f32p(row_z),
+    )
+    if status != 0:
+        raise ValueError("oracle sampler rejected its inputs")
+    return nodes[:, :max_depth], length, bonus, row_m, row_z
+
+
+def ancestral_walk(parents: Sequence[int], tokens: Sequence[int],
+                   posterior_tokens: Sequence[int]):
+    """Tree walk of sampling.py:937-950 on pre-drawn per-node tokens."""
+    children = {
+        (int(parents[node]), int(tokens[node - 1])): node
+        for node in range(1, len(parents))
+    }
+    nodes, accepted = [], []
+    node = 0
+    bonus = int(posterior_tokens[node])
+    while (node, bonus) in children:
+        node = children[node, bonus]
+        nodes.append(node)
+        accepted.append(bonus)
+        bonus = int(posterior_tokens[node])
+    return nodes, accepted, bonus
+
+
+# --------------------------------------------------------------------------
+# Packing (tree.py:19-26, CTBD:500-546)
+# --------------------------------------------------------------------------
+
+def visibility(parents: Sequence[int]) -> np.ndarray:
+    """Ancestor-or-self matrix, row i = row parent[i] plus the diagonal."""
+    n = len(parents)
+    visible = np.zeros((n, n), dtype=bool)
+    visible[0, 0] = True
+    for i in range(1, n):
+        visible[i] = visible[parents[i]]
+        visible[i, i] = True
+    return visible
+
+
+def packed_dense_mask(prefix_lengths: Sequence[int],
+                      parents_list: Sequence[Sequence[int]]) -> np.ndarray:
+    """Dense additive mask [R, P+R] (0 visible, -inf hidden) of CTBD:500-546.
+
+    Request i's rows see keys [c_i, c_i+L_i) of the packed prefix and the
+    packed tree keys P + q_i + j for every ancestor-or-self j.
+    """
+    lengths = [int(v) for v in prefix_lengths]
+    rows = [len(p) for p in parents_list]
+    total_prefix = sum(lengths)
+    total_rows = sum(rows)
+    mask = np.full((total_rows, total_prefix + total_rows), -np.inf, np.float32)
+    cache_offset = 0
+    query_offset = 0
+    for length, parents in zip(lengths, parents_list):
+        n = len(parents)
+        mask[query_offset:query_offset + n, cache_offset:cache_offset + length] = 0
+        block = mask[query_offset:query_offset + n,
+                     total_prefix + query_offset:total_prefix + query_offset + n]
+        block[visibility(parents)] = 0
+        cache_offset += length
+        query_offset += n
+    return mask
+
+
+def packed_ids_positions(roots: Sequence[int], tokens_list, depths_list,
+                         round_prefix_lengths: Sequence[int]):
+    """ids = [root] + tokens, positions = round_prefix_len + depth (CTBD:521-532)."""
+    ids = []
+    positions = []
+    for root, tokens, depths, prefix in zip(roots, tokens_list, depths_list,
+                                            round_prefix_lengths):
+        ids.extend([int(root)] + [int(t) for t in tokens])
+        positions.extend(int(prefix) + int(d) for d in depths)
+    return np.asarray(ids, np.int64), np.asarray(positions, np.int64)
+
+
+# --------------------------------------------------------------------------
+# Attention (transformers sdpa_attention_forward with an explicit mask)
+# --------------------------------------------------------------------------
+
+def attention_dense(q, k_prefix_list, v_prefix_list, k_tree, v_tree,
+                    parents_list, scale: float | None = None):
+    """Reference packed wave: one dense masked SDPA over all P+R keys.
+
+    q [R, Hq, D]; k/v_prefix_list[i] [Hkv, L_i, D]; k/v_tree [R, Hkv, D].
+    All inputs are upcast to fp32 (they hold bf16 values).  Returns [R, Hq, D]
+    fp32.  Mirrors _pack_cache_sequence + _packed_block_inputs + repeat_kv +
+    F.scaled_dot_product_attention(attn_mask=mask) (CTBD:313-361, :500-546).
+    """
+    import torch
+    q = torch.as_tensor(q).float()
+    rows, hq, dim = q.shape
+    hkv = k_tree.shape[1]
+    group = hq // hkv
+    lengths = [int(k.shape[1]) for k in k_prefix_list]
+    keys = torch.cat([torch.as_tensor(k).float() for k in k_prefix_list]
+                     + [torch.as_tensor(k_tree).float().transpose(0, 1)], dim=1)
+    values = torch.cat([torch.as_tensor(v).float() for v in v_prefix_list]
+                       + [torch.as_tensor(v_tree).float().transpose(0, 1)], dim=1)
+    mask = torch.from_numpy(packed_dense_mask(lengths, parents_list))
+    keys = keys.repeat_interleave(group, dim=0)
+    values = values.repeat_interleave(group, dim=0)
+    scale = dim ** -0.5 if scale is None else scale
+    out = torch.nn.functional.scaled_dot_product_attention(
+        q.transpose(0, 1).unsqueeze(0), keys.unsqueeze(0), values.unsqueeze(0),
+        attn_mask=mask, scale=scale,
+    )
+    return out[0].transpose(0, 1).contiguous()
+
+
+def attention_per_request(q, k_prefix_list, v_prefix_list, k_tree, v_tree,
+                          row_offset, parents_list, scale: float | None = None,
+                          requests: Sequence[int] | None = None):
+    """Same math as attention_dense restricted to each request's own keys.
+
+    Returns a dict request -> [n_i, Hq, D] fp32 (only ``requests`` if given).
+    """
+    import torch
+    q = torch.as_tensor(q)
+    rows, hq, dim = q.shape
+    hkv = k_tree.shape[1]
+    group = hq // hkv
+    scale = dim ** -0.5 if scale is None else scale
+    out = {}
+    selected = range(len(parents_list)) if requests is None else requests
+    for i in selected:
+        r0, r1 = int(row_offset[i]), int(row_offset[i + 1])
+        n = r1 - r0
+        kp = torch.as_tensor(k_prefix_list[i]).float()
+        vp = torch.as_tensor(v_prefix_list[i]).float()
+        kt = torch.as_tensor(k_tree[r0:r1]).float().transpose(0, 1)
+        vt = torch.as_tensor(v_tree[r0:r1]).float().transpose(0, 1)
+        keys = torch.cat([kp, kt], dim=1).repeat_interleave(group, dim=0)
+        values = torch.cat([vp, vt], dim=1).repeat_interleave(group, dim=0)
+        length = kp.shape[1]
+        mask = torch.full((n, length + n), -math.inf)
+        mask[:, :length] = 0
+        vis = torch.from_numpy(visibility(parents_list[i]))
+        mask[:, length:][vis] = 0
+        qi = q[r0:r1].float().transpose(0, 1).unsqueeze(0)
+        o = torch.nn.functional.scaled_dot_product_attention(
+            qi, keys.unsqueeze(0), values.unsqueeze(0), attn_mask=mask,
+            scale=scale,
+        )
+        out[i] = o[0].transpose(0, 1).contiguous()
+    return out
+
+
+def attention_bruteforce(q, k_prefix_list, v_prefix_list, k_tree, v_tree,
+                         row_offset, parents_list, scale: float | None = None):
+    """Explicit per-row, per-head softmax loops in float64 (tiny cases only)."""
+    q = np.asarray(q, np.float64)
+    rows, hq, dim = q.shape
+    hkv = k_tree.shape[1]
+    group = hq // hkv
+    scale = dim ** -0.5 if scale is None else scale
+    out = np.zeros((rows, hq, dim))
+    for i, parents in enumerate(parents_list):
+        r0 = int(row_offset[i])
+        kp = np.asarray(k_prefix_list[i], np.float64)
+        vp = np.asarray(v_prefix_list[i], np.float64)
+        for local in range(len(parents)):
+            ancestors = []
+            node = local
+            while node >= 0:
+                ancestors.append(node)
+                node = parents[node]
+            for h in range(hq):
+                g = h // group
+                keys = [kp[g, t] for t in range(kp.shape[1])]
+                vals = [vp[g, t] for t in range(vp.shape[1])]
+                for a in sorted(ancestors):
+                    keys.append(np.asarray(k_tree[r0 + a, g], np.float64))
+                    vals.append(np.asarray(v_tree[r0 + a, g], np.float64))
+                scores = np.array([q[r0 + local, h] @ k for k in keys]) * scale
+                weights = np.exp(scores - scores.max())
+                weights /= weights.sum()
+                out[r0 + local, h] = weights @ np.stack(vals)
+    return out
+
+
+# --------------------------------------------------------------------------
+# KV commit (CTBD:215-261, keep rule CTBD:2108-2109)
+# --------------------------------------------------------------------------
+
+def kv_commit(arena_k: np.ndarray, arena_v: np.ndarray, lengths: np.ndarray,
+              capacity: int, slots: Sequence[int], tree_k: np.ndarray,
+              tree_v: np.ndarray, row_offset: Sequence[int],
+              keep_rows: Sequence[Sequence[int]]):
+    """Scatter kept tree rows into the arena and advance lengths, in place.
+
+    arena_k/v [layers, Hkv, slots*capacity, D]; tree_k/v [layers, R, Hkv, D];
+    keep_rows[i] = [0] + accepted local nodes.  For t < len(keep_i):
+      arena[:, :, slot_i*cap + len_i + t] = tree[:, row_offset[i] + keep_i[t]].
+    Raises RuntimeError when len_i + len(keep_i) > capacity (CTBD:235-236).
+    """
+    for i, keep in enumerate(keep_rows):
+        slot = int(slots[i])
+        if int(lengths[slot]) + len(keep) > capacity:
+            raise RuntimeError("Persistent request KV capacity exhausted")
+    for i, keep in enumerate(keep_rows):
+        slot = int(slots[i])
+        base = slot * capacity + int(lengths[slot])
+        for t, row in enumerate(keep):
+            src = int(row_offset[i]) + int(row)
+            arena_k[:, :, base + t] = tree_k[:, src]
+            arena_v[:, :, base + t] = tree_v[:, src]
+        lengths[slot] += len(keep)
+    return lengths
+
+
+def cpu_threads() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1

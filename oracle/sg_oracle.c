@@ -1,0 +1,328 @@
+/*
+ * sg_oracle.c -- CPU restatement of the temperature-1 tree rejection sampler.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker for the HIP sampler in
+ * specgrove_amd/csrc/tree_sample.hip.  Only tests/, __graft_entry__.smoke()
+ * and bench.py's CPU-baseline leg may load the library built from it.  The
+ * product path never calls it.
+ *
+ * What it restates (reference files, relative to the reference snapshot):
+ *   - the ancestral acceptance law of tree_verify_ancestral_batched
+ *     (code/natural/src/gbv_experiments/sampling.py:903-950): a draw from the
+ *     node's target row either follows an outgoing tree edge (accept that
+ *     child) or ends the walk and becomes the bonus token;
+ *   - the explicit-uniform sparse-exit layout of the reference's CUDA sampler
+ *     (code/natural/src/gbv_experiments/fused_tree_sampling.py:683-824):
+ *     uniform u[2d] routes over the children's cumulative mass in edge order,
+ *     u[2d+1] draws the exit token from the complement of the children, and the
+ *     fallback is the largest non-child token (:804-818);
+ *   - the inverse-CDF rule "first token whose running mass exceeds u * total"
+ *     (fused_tree_sampling.py:2607-2612).
+ *
+ * The reference accumulates in fp64 with CUB's reduction order.  This build
+ * computes in fp32 with its own exp and a fixed reduction order so that the
+ * CPU and the GPU produce the same bits.  The order is:
+ *
+ *   exp:   E(x) = 0 for x < -87 (or NaN); otherwise Cody-Waite reduction
+ *          x = n*ln2 + r (n = rint(x*log2e), ln2 split hi/lo, both by fma),
+ *          degree-6 Taylor polynomial for e^r in Horner form with fma, and an
+ *          exact scale by 2^n built from the exponent bits.
+ *   token t of a row is addressed as t = 2048*s + 256*j + 4*l + c
+ *          (slab s, line j in [0,8), lane l in [0,64), component c in [0,4)).
+ *   row stats (m, Z):
+ *          per slab: m_s = max; lane partial a_c = sum over j (ascending) of
+ *          E(x - m_s); lane sum (a0+a1)+(a2+a3); slab sum by an xor butterfly
+ *          over the 64 lanes (distances 32,16,8,4,2,1).  Slab (m_s, Z_s) pairs
+ *          are merged into lane (s mod 64) in ascending s, then the 64 lane
+ *          pairs are merged by the same xor butterfly; merge(a,b) =
+ *          (M, a.z*E(a.m-M) + b.z*E(b.m-M)), M = max(a.m, b.m).
+ *   routing at node v: children in ascending node order; S += E(x[tok]-m_v);
+ *          accept the first child with u[2d]*Z_v < S.
+ *   exit at node v: e_t = 0 for child tokens, else E(x_t - m_v);
+ *          group sum ((e0+e1)+e2)+e3 per (s,j,l); inclusive Kogge-Stone scan
+ *          over the 64 lanes of a line (distances 1..32); line prefix and slab
+ *          prefix sequential; complement total C = last slab prefix;
+ *          threshold u[2d+1]*C; the bonus is the smallest non-child token t
+ *          whose running value ((PX_s + LX_sj) + EX_sjl) + e_c0 + ... + e_c
+ *          exceeds the threshold; fallback = largest non-child token.
+ *
+ * All arithmetic is IEEE binary32 with round-to-nearest-even; the build uses
+ * -ffp-contract=off so that only the explicit fmaf calls fuse.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#define SGO_LANES 64
+#define SGO_SLAB 2048
+#define SGO_LINE 256
+#define SGO_LINES_PER_SLAB 8
+
+#define SGO_LOG2E 0x1.715476p+0f
+#define SGO_LN2_HI 0x1.62e4p-1f
+#define SGO_LN2_LO 0x1.7f7d1cp-20f
+#define SGO_C6 0x1.6c16c2p-10f
+#define SGO_C5 0x1.111112p-7f
+#define SGO_C4 0x1.555556p-5f
+#define SGO_C3 0x1.555556p-3f
+#define SGO_EXP_LO (-87.0f)
+#define SGO_EXP_HI 88.0f
+
+/* Error codes shared with the product ABI. */
+#define SGO_OK 0
+#define SGO_EINVAL (-1)
+
+float sgo_exp(float x) {
+  if (!(x >= SGO_EXP_LO)) return 0.0f;
+  if (x > SGO_EXP_HI) return INFINITY;
+  float n = rintf(x * SGO_LOG2E);
+  float r = fmaf(-n, SGO_LN2_HI, x);
+  r = fmaf(-n, SGO_LN2_LO, r);
+  float p = SGO_C6;
+  p = fmaf(p, r, SGO_C5);
+  p = fmaf(p, r, SGO_C4);
+  p = fmaf(p, r, SGO_C3);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  int32_t bits = ((int32_t)n + 127) << 23;
+  float scale;
+  memcpy(&scale, &bits, sizeof(scale));
+  return p * scale;
+}
+
+typedef struct {
+  float m;
+  float z;
+} sgo_mz;
+
+static sgo_mz sgo_merge(sgo_mz a, sgo_mz b) {
+  sgo_mz out;
+  float mx = fmaxf(a.m, b.m);
+  if (mx == -INFINITY) {
+    out.m = -INFINITY;
+    out.z = 0.0f;
+    return out;
+  }
+  float left = a.z * sgo_exp(a.m - mx);
+  float right = b.z * sgo_exp(b.m - mx);
+  out.m = mx;
+  out.z = left + right;
+  return out;
+}
+
+static float sgo_butterfly_sum(float* v) {
+  float t[SGO_LANES];
+  for (int d = 32; d >= 1; d >>= 1) {
+    for (int l = 0; l < SGO_LANES; ++l) t[l] = v[l] + v[l ^ d];
+    memcpy(v, t, sizeof(t));
+  }
+  return v[0];
+}
+
+static sgo_mz sgo_slab_stats(const float* x, int64_t vocab, int64_t slab) {
+  const int64_t base = slab * SGO_SLAB;
+  float m = -INFINITY;
+  for (int64_t t = base; t < base + SGO_SLAB && t < vocab; ++t) m = fmaxf(m, x[t]);
+  sgo_mz out;
+  if (m == -INFINITY) {
+    out.m = -INFINITY;
+    out.z = 0.0f;
+    return out;
+  }
+  float lane[SGO_LANES];
+  for (int l = 0; l < SGO_LANES; ++l) {
+    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < SGO_LINES_PER_SLAB; ++j) {
+      for (int c = 0; c < 4; ++c) {
+        int64_t t = base + (int64_t)SGO_LINE * j + 4 * l + c;
+        if (t < vocab) a[c] = a[c] + sgo_exp(x[t] - m);
+      }
+    }
+    lane[l] = (a[0] + a[1]) + (a[2] + a[3]);
+  }
+  out.m = m;
+  out.z = sgo_butterfly_sum(lane);
+  return out;
+}
+
+/* Canonical (max, sum of exp) of one logits row. */
+void sgo_row_stats(const float* x, int64_t vocab, float* out_m, float* out_z) {
+  sgo_mz lane[SGO_LANES];
+  for (int l = 0; l < SGO_LANES; ++l) {
+    lane[l].m = -INFINITY;
+    lane[l].z = 0.0f;
+  }
+  const int64_t slabs = (vocab + SGO_SLAB - 1) / SGO_SLAB;
+  for (int64_t s = 0; s < slabs; ++s) {
+    int l = (int)(s % SGO_LANES);
+    lane[l] = sgo_merge(lane[l], sgo_slab_stats(x, vocab, s));
+  }
+  sgo_mz t[SGO_LANES];
+  for (int d = 32; d >= 1; d >>= 1) {
+    for (int l = 0; l < SGO_LANES; ++l) t[l] = sgo_merge(lane[l], lane[l ^ d]);
+    memcpy(lane, t, sizeof(t));
+  }
+  *out_m = lane[0].m;
+  *out_z = lane[0].z;
+}
+
+static int sgo_is_child_token(int64_t t, const int32_t* child_tokens, int child_count) {
+  for (int k = 0; k < child_count; ++k)
+    if (child_tokens[k] == t) return 1;
+  return 0;
+}
+
+/* Complement draw of one row: returns the bonus token and stores C. */
+int32_t sgo_complement_draw(const float* x, int64_t vocab, float m,
+                            const int32_t* child_tokens, int child_count,
+                            float u, float* out_total) {
+  const int64_t slabs = (vocab + SGO_SLAB - 1) / SGO_SLAB;
+  /* Pass 1: per-line Kogge-Stone totals, line and slab prefixes. */
+  float* slab_prefix = (float*)__builtin_alloca(sizeof(float) * (size_t)(slabs + 1));
+  float lp[SGO_LINES_PER_SLAB + 1];
+  slab_prefix[0] = 0.0f;
+  for (int64_t s = 0; s < slabs; ++s) {
+    lp[0] = 0.0f;
+    for (int j = 0; j < SGO_LINES_PER_SLAB; ++j) {
+      float v[SGO_LANES], w[SGO_LANES];
+      for (int l = 0; l < SGO_LANES; ++l) {
+        float g = 0.0f;
+        float e[4];
+        for (int c = 0; c < 4; ++c) {
+          int64_t t = s * SGO_SLAB + (int64_t)SGO_LINE * j + 4 * l + c;
+          e[c] = (t < vocab && !sgo_is_child_token(t, child_tokens, child_count))
+                     ? sgo_exp(x[t] - m) : 0.0f;
+        }
+        g = ((e[0] + e[1]) + e[2]) + e[3];
+        v[l] = g;
+      }
+      for (int d = 1; d < SGO_LANES; d <<= 1) {
+        for (int l = 0; l < SGO_LANES; ++l) w[l] = (l >= d) ? v[l] + v[l - d] : v[l];
+        memcpy(v, w, sizeof(w));
+      }
+      lp[j + 1] = lp[j] + v[SGO_LANES - 1];
+    }
+    slab_prefix[s + 1] = slab_prefix[s] + lp[SGO_LINES_PER_SLAB];
+  }
+  const float total = slab_prefix[slabs];
+  if (out_total) *out_total = total;
+  const float threshold = u * total;
+  /* Pass 2: first token whose running value exceeds the threshold. */
+  for (int64_t s = 0; s < slabs; ++s) {
+    lp[0] = 0.0f;
+    float lines_incl[SGO_LINES_PER_SLAB][SGO_LANES];
+    float e_all[SGO_LINES_PER_SLAB][SGO_LANES][4];
+    for (int j = 0; j < SGO_LINES_PER_SLAB; ++j) {
+      float v[SGO_LANES], w[SGO_LANES];
+      for (int l = 0; l < SGO_LANES; ++l) {
+        for (int c = 0; c < 4; ++c) {
+          int64_t t = s * SGO_SLAB + (int64_t)SGO_LINE * j + 4 * l + c;
+          e_all[j][l][c] = (t < vocab && !sgo_is_child_token(t, child_tokens, child_count))
+                               ? sgo_exp(x[t] - m) : 0.0f;
+        }
+        v[l] = ((e_all[j][l][0] + e_all[j][l][1]) + e_all[j][l][2]) + e_all[j][l][3];
+      }
+      for (int d = 1; d < SGO_LANES; d <<= 1) {
+        for (int l = 0; l < SGO_LANES; ++l) w[l] = (l >= d) ? v[l] + v[l - d] : v[l];
+        memcpy(v, w, sizeof(w));
+      }
+      memcpy(lines_incl[j], v, sizeof(v));
+      lp[j + 1] = lp[j] + v[SGO_LANES - 1];
+    }
+    for (int j = 0; j < SGO_LINES_PER_SLAB; ++j) {
+      for (int l = 0; l < SGO_LANES; ++l) {
+        float excl = l ? lines_incl[j][l - 1] : 0.0f;
+        float run = (slab_prefix[s] + lp[j]) + excl;
+        for (int c = 0; c < 4; ++c) {
+          int64_t t = s * SGO_SLAB + (int64_t)SGO_LINE * j + 4 * l + c;
+          if (t >= vocab) break;
+          run = run + e_all[j][l][c];
+          if (!sgo_is_child_token(t, child_tokens, child_count) && run > threshold)
+            return (int32_t)t;
+        }
+      }
+    }
+  }
+  for (int64_t t = vocab - 1; t >= 0; --t)
+    if (!sgo_is_child_token(t, child_tokens, child_count)) return (int32_t)t;
+  return -1;
+}
+
+/*
+ * Sample every request of a packed wave.
+ *   logits      [rows, row_stride] fp32 (only the first vocab entries used)
+ *   row_offset  [n+1]   packed row range of request i
+ *   parent      [rows]  request-local parent index, -1 for each request's root
+ *   token       [rows]  draft token of each node (ignored for roots)
+ *   uniforms    [n, uniform_stride] fp32, u[2d] routes and u[2d+1] exits at depth d
+ *   max_depth   accept_nodes holds max_depth entries per request
+ * Outputs: accept_nodes [n, max_depth] (local node ids, -1 padded),
+ *          accept_len [n], bonus [n], row_m / row_z [rows] (may be NULL).
+ * Returns SGO_OK or SGO_EINVAL.
+ */
+int sgo_tree_sample(const float* logits, int64_t row_stride, int64_t vocab,
+                    int32_t num_requests, const int32_t* row_offset,
+                    const int32_t* parent, const int32_t* token,
+                    const float* uniforms, int32_t uniform_stride,
+                    int32_t max_depth, int32_t* accept_nodes,
+                    int32_t* accept_len, int32_t* bonus, float* row_m,
+                    float* row_z) {
+  if (num_requests < 0 || vocab < 1 || max_depth < 0) return SGO_EINVAL;
+  const int32_t rows = row_offset[num_requests];
+  for (int32_t r = 0; r < rows; ++r) {
+    float m, z;
+    sgo_row_stats(logits + (int64_t)r * row_stride, vocab, &m, &z);
+    if (row_m) row_m[r] = m;
+    if (row_z) row_z[r] = z;
+  }
+  for (int32_t i = 0; i < num_requests; ++i) {
+    const int32_t r0 = row_offset[i];
+    const int32_t n = row_offset[i + 1] - r0;
+    const float* u = uniforms + (int64_t)i * uniform_stride;
+    for (int32_t k = 0; k < max_depth; ++k) accept_nodes[(int64_t)i * max_depth + k] = -1;
+    int32_t v = 0, depth = 0;
+    int32_t children[1024];
+    int32_t child_tokens[1024];
+    for (;;) {
+      if (2 * depth + 1 >= uniform_stride || n > 1024) return SGO_EINVAL;
+      const float* x = logits + (int64_t)(r0 + v) * row_stride;
+      float m, z;
+      sgo_row_stats(x, vocab, &m, &z);
+      int count = 0;
+      for (int32_t w = v + 1; w < n; ++w) {
+        if (parent[r0 + w] == v) {
+          children[count] = w;
+          child_tokens[count] = token[r0 + w];
+          ++count;
+        }
+      }
+      const float route_threshold = u[2 * depth] * z;
+      float cumulative = 0.0f;
+      int32_t accepted = -1;
+      for (int k = 0; k < count; ++k) {
+        cumulative = cumulative + sgo_exp(x[child_tokens[k]] - m);
+        if (route_threshold < cumulative) {
+          accepted = children[k];
+          break;
+        }
+      }
+      if (accepted >= 0) {
+        if (depth >= max_depth) return SGO_EINVAL;
+        accept_nodes[(int64_t)i * max_depth + depth] = accepted;
+        v = accepted;
+        ++depth;
+        continue;
+      }
+      accept_len[i] = depth;
+      bonus[i] = sgo_complement_draw(x, vocab, m, child_tokens, count, u[2 * depth + 1], 0);
+      break;
+    }
+  }
+  return SGO_OK;
+}
+
+/* Vectorised E(x) for tests of the exp restatement. */
+void sgo_exp_array(const float* x, float* out, int64_t count) {
+  for (int64_t k = 0; k < count; ++k) out[k] = sgo_exp(x[k]);
+}

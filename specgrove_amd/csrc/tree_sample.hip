@@ -1,0 +1,493 @@
+// Temperature-1 tree rejection sampling over a packed verification wave.
+//
+// Law: tree_verify_ancestral_batched (reference sampling.py:903-950) -- from a
+// node's target row, a draw either follows an outgoing tree edge (the child is
+// accepted and the walk continues there) or ends the walk as the bonus token.
+// Uniform layout and fallbacks follow the reference's sparse-exit sampler
+// (fused_tree_sampling.py:683-824): u[2d] routes over the children's
+// cumulative mass in edge order, u[2d+1] draws from the complement of the
+// children (the whole row at a leaf), and the fallback is the largest
+// non-child token (:804-818).
+//
+// Arithmetic contract (bit-exact with the CPU restatement): binary32 only,
+// no contraction except the explicit fmas of sg_exp, and the fixed reduction
+// order below.  A row is addressed as token t = 2048*s + 256*j + 4*l + c
+// (slab s, line j, lane l, component c); one wavefront owns a slab at a time
+// and reads it as 8 coalesced 1 KiB float4 lines.
+//
+//   row stats: slab max; lane partials a_c = sum_j E(x - m_s); lane sum
+//     (a0+a1)+(a2+a3); xor butterfly over the wave; slab (m, Z) merged into
+//     lane s%64; final xor butterfly merge over the 64 lanes.
+//   routing:  S += E(x[child token] - m) over children in node order; accept
+//     the first child with u*Z < S.
+//   exit: group sums ((e0+e1)+e2)+e3, inclusive Kogge-Stone scan over the 64
+//     lanes of a line, sequential line and slab prefixes; the bonus is the
+//     first non-child token whose running value exceeds u*C.
+#pragma clang fp contract(off)
+
+#include <limits.h>
+
+#include "sg_common.h"
+
+namespace sg {
+namespace {
+
+constexpr int kSlab = 2048;
+constexpr int kLine = 256;
+constexpr int kLinesPerSlab = 8;
+constexpr int kMaxSlabs = 256;  // vocab <= 524288
+constexpr int kStatsThreads = 256;
+constexpr int kWalkThreads = 1024;
+constexpr int kWalkWaves = kWalkThreads / kWave;
+constexpr int kMaxTreeRows = 1024;
+
+#define SG_LOG2E 0x1.715476p+0f
+#define SG_LN2_HI 0x1.62e4p-1f
+#define SG_LN2_LO 0x1.7f7d1cp-20f
+#define SG_C6 0x1.6c16c2p-10f
+#define SG_C5 0x1.111112p-7f
+#define SG_C4 0x1.555556p-5f
+#define SG_C3 0x1.555556p-3f
+
+// E(x): 0 below -87 (and for NaN), Cody-Waite reduction with a split ln2,
+// degree-6 Taylor polynomial in Horner form, exact scale by 2^n.
+__device__ __forceinline__ float sg_exp(float x) {
+  const bool live = x >= -87.0f;
+  const float xc = fminf(fmaxf(x, -87.0f), 88.0f);
+  const float n = __builtin_rintf(xc * SG_LOG2E);
+  float r = __builtin_fmaf(-n, SG_LN2_HI, xc);
+  r = __builtin_fmaf(-n, SG_LN2_LO, r);
+  float p = SG_C6;
+  p = __builtin_fmaf(p, r, SG_C5);
+  p = __builtin_fmaf(p, r, SG_C4);
+  p = __builtin_fmaf(p, r, SG_C3);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  const int bits = (static_cast<int>(n) + 127) << 23;
+  float y = p * __int_as_float(bits);
+  y = (x > 88.0f) ? __builtin_inff() : y;
+  return live ? y : 0.0f;
+}
+
+struct MZ {
+  float m;
+  float z;
+};
+
+__device__ __forceinline__ MZ merge_mz(MZ a, MZ b) {
+  MZ out;
+  out.m = fmaxf(a.m, b.m);
+  const float left = a.z * sg_exp(a.m - out.m);
+  const float right = b.z * sg_exp(b.m - out.m);
+  out.z = (out.m == -__builtin_inff()) ? 0.0f : left + right;
+  return out;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v = fmaxf(v, __shfl_xor(v, d));
+  return v;
+}
+
+__device__ __forceinline__ float wave_butterfly_sum(float v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v = v + __shfl_xor(v, d);
+  return v;
+}
+
+// Lane l of the wave loads tokens 2048*s + 256*j + 4*l + c into v[4*j + c];
+// tokens at or beyond vocab read as -inf (they contribute E = 0).
+template <bool kVec4>
+__device__ __forceinline__ void load_slab(const float* __restrict__ x, int vocab,
+                                          int slab, int lane, float v[32]) {
+  const int base = slab * kSlab + 4 * lane;
+  if (kVec4) {
+#pragma unroll
+    for (int j = 0; j < kLinesPerSlab; ++j) {
+      const int t = base + kLine * j;
+      if (t < vocab) {
+        const float4 q = *reinterpret_cast<const float4*>(x + t);
+        v[4 * j + 0] = q.x;
+        v[4 * j + 1] = q.y;
+        v[4 * j + 2] = q.z;
+        v[4 * j + 3] = q.w;
+      } else {
+        v[4 * j + 0] = v[4 * j + 1] = v[4 * j + 2] = v[4 * j + 3] = -__builtin_inff();
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kLinesPerSlab; ++j) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int t = base + kLine * j + c;
+        v[4 * j + c] = (t < vocab) ? x[t] : -__builtin_inff();
+      }
+    }
+  }
+}
+
+template <bool kVec4>
+__device__ MZ wave_row_stats(const float* __restrict__ x, int vocab, int lane) {
+  const int slabs = (vocab + kSlab - 1) / kSlab;
+  MZ acc = {-__builtin_inff(), 0.0f};
+  for (int s = 0; s < slabs; ++s) {
+    float v[32];
+    load_slab<kVec4>(x, vocab, s, lane, v);
+    float m = v[0];
+#pragma unroll
+    for (int k = 1; k < 32; ++k) m = fmaxf(m, v[k]);
+    m = wave_max(m);
+    MZ slab = {m, 0.0f};
+    if (m != -__builtin_inff()) {
+      float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+#pragma unroll
+      for (int j = 0; j < kLinesPerSlab; ++j) {
+        a0 = a0 + sg_exp(v[4 * j + 0] - m);
+        a1 = a1 + sg_exp(v[4 * j + 1] - m);
+        a2 = a2 + sg_exp(v[4 * j + 2] - m);
+        a3 = a3 + sg_exp(v[4 * j + 3] - m);
+      }
+      slab.z = wave_butterfly_sum((a0 + a1) + (a2 + a3));
+    }
+    const MZ merged = merge_mz(acc, slab);
+    if (lane == (s & (kWave - 1))) acc = merged;
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    MZ other;
+    other.m = __shfl_xor(acc.m, d);
+    other.z = __shfl_xor(acc.z, d);
+    acc = merge_mz(acc, other);
+  }
+  return acc;
+}
+
+// One wavefront per row, four rows per workgroup.
+template <bool kVec4>
+__global__ __launch_bounds__(kStatsThreads) void row_stats_kernel(
+    const float* __restrict__ logits, int64_t row_stride, int vocab, int rows,
+    float* __restrict__ row_max, float* __restrict__ row_sum) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int row = blockIdx.x * (kStatsThreads / kWave) + (threadIdx.x / kWave);
+  if (row >= rows) return;
+  const MZ r = wave_row_stats<kVec4>(logits + row_stride * row, vocab, lane);
+  if (lane == 0) {
+    row_max[row] = r.m;
+    row_sum[row] = r.z;
+  }
+}
+
+// Child-token bitmask of this lane in slab s: bit 4*j+c marks token
+// 2048*s + 256*j + 4*lane + c as a child token of the exit node.
+__device__ __forceinline__ uint32_t child_bits(const int* child_tok, int count,
+                                               int slab, int lane) {
+  uint32_t bits = 0;
+  for (int k = 0; k < count; ++k) {
+    const int t = child_tok[k];
+    const int local = t - slab * kSlab;
+    if (local >= 0 && local < kSlab && ((local >> 2) & (kWave - 1)) == lane)
+      bits |= 1u << (4 * (local >> 8) + (local & 3));
+  }
+  return bits;
+}
+
+// Exit-row values of one slab: e = 0 for child tokens and tokens >= vocab.
+template <bool kVec4>
+__device__ __forceinline__ void exit_values(const float* __restrict__ x, int vocab,
+                                            float m, int slab, int lane,
+                                            uint32_t bits, float e[32]) {
+  load_slab<kVec4>(x, vocab, slab, lane, e);
+#pragma unroll
+  for (int k = 0; k < 32; ++k) {
+    const float val = sg_exp(e[k] - m);
+    e[k] = ((bits >> k) & 1u) ? 0.0f : val;
+  }
+}
+
+// Inclusive Kogge-Stone scan of the group sums of each line; returns the
+// per-line inclusive values of this lane in incl[j] and the line totals.
+__device__ __forceinline__ void line_scans(const float e[32], int lane,
+                                           float incl[kLinesPerSlab],
+                                           float total[kLinesPerSlab]) {
+#pragma unroll
+  for (int j = 0; j < kLinesPerSlab; ++j) {
+    float g = ((e[4 * j + 0] + e[4 * j + 1]) + e[4 * j + 2]) + e[4 * j + 3];
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const float up = __shfl_up(g, d);
+      g = (lane >= d) ? g + up : g;
+    }
+    incl[j] = g;
+    total[j] = __shfl(g, kWave - 1);
+  }
+}
+
+template <bool kVec4>
+__global__ __launch_bounds__(kWalkThreads) void tree_walk_kernel(SgTreeSampleArgs a) {
+  __shared__ int s_child_node[kMaxTreeRows];
+  __shared__ int s_child_tok[kMaxTreeRows];
+  __shared__ int s_wave_count[kWalkWaves];
+  __shared__ float s_slab_total[kMaxSlabs];
+  __shared__ float s_slab_prefix[kMaxSlabs + 1];
+  __shared__ int s_child_count;
+  __shared__ int s_accepted;
+  __shared__ int s_candidate;
+  __shared__ float s_threshold;
+
+  const int req = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int r0 = a.row_offset_dev[req];
+  const int n = a.row_offset_dev[req + 1] - r0;
+  const float* __restrict__ u = a.uniforms_dev + static_cast<int64_t>(a.uniform_stride) * req;
+  int32_t* nodes_out = a.accept_nodes_dev + static_cast<int64_t>(a.max_depth) * req;
+  if (n < 1 || n > kMaxTreeRows) {
+    if (tid == 0) {
+      a.accept_len_dev[req] = -1;
+      a.bonus_dev[req] = -1;
+      if (a.status_dev) atomicExch(a.status_dev, SG_EINVAL);
+    }
+    return;
+  }
+  for (int k = tid; k < a.max_depth; k += kWalkThreads) nodes_out[k] = -1;
+
+  int v = 0;
+  int depth = 0;
+  bool broken = false;
+  for (;;) {
+    __syncthreads();
+    // Children of v in ascending node order.
+    const bool is_child = tid < n && tid > v && a.parent_dev[r0 + tid] == v;
+    const uint64_t mask = __ballot(is_child);
+    if (lane == 0) s_wave_count[wave] = __popcll(mask);
+    __syncthreads();
+    int offset = 0;
+    int total = 0;
+    for (int w = 0; w < kWalkWaves; ++w) {
+      offset += (w < wave) ? s_wave_count[w] : 0;
+      total += s_wave_count[w];
+    }
+    if (is_child) {
+      const int pos = offset + __popcll(mask & ((1ull << lane) - 1ull));
+      s_child_node[pos] = tid;
+      s_child_tok[pos] = a.token_dev[r0 + tid];
+    }
+    if (tid == 0) s_child_count = total;
+    __syncthreads();
+    if (tid == 0) {
+      int accepted = -1;
+      if (2 * depth + 1 >= a.uniform_stride) {
+        accepted = -2;
+      } else {
+        const int64_t row = r0 + v;
+        const float* __restrict__ x = a.logits_dev + a.logits_row_stride * row;
+        const float m = a.row_max_dev[row];
+        const float threshold = u[2 * depth] * a.row_sum_dev[row];
+        float cumulative = 0.0f;
+        for (int k = 0; k < s_child_count; ++k) {
+          cumulative = cumulative + sg_exp(x[s_child_tok[k]] - m);
+          if (threshold < cumulative) {
+            accepted = s_child_node[k];
+            break;
+          }
+        }
+        if (accepted >= 0 && depth >= a.max_depth) accepted = -2;
+      }
+      s_accepted = accepted;
+    }
+    __syncthreads();
+    const int accepted = s_accepted;
+    if (accepted == -2) {
+      broken = true;
+      break;
+    }
+    if (accepted < 0) break;
+    if (tid == 0) nodes_out[depth] = accepted;
+    v = accepted;
+    ++depth;
+  }
+  if (broken) {
+    if (tid == 0) {
+      a.accept_len_dev[req] = -1;
+      a.bonus_dev[req] = -1;
+      if (a.status_dev) atomicExch(a.status_dev, SG_EINVAL);
+    }
+    return;
+  }
+
+  // Exit at v: draw the bonus from the complement of v's children.
+  const int64_t row = r0 + v;
+  const float* __restrict__ x = a.logits_dev + a.logits_row_stride * row;
+  const float m = a.row_max_dev[row];
+  const int count = s_child_count;
+  const int slabs = (a.vocab + kSlab - 1) / kSlab;
+
+  for (int s = wave; s < slabs; s += kWalkWaves) {
+    float e[32], incl[kLinesPerSlab], total[kLinesPerSlab];
+    exit_values<kVec4>(x, a.vocab, m, s, lane, child_bits(s_child_tok, count, s, lane), e);
+    line_scans(e, lane, incl, total);
+    float lp = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kLinesPerSlab; ++j) lp = lp + total[j];
+    if (lane == 0) s_slab_total[s] = lp;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float prefix = 0.0f;
+    for (int s = 0; s < slabs; ++s) {
+      s_slab_prefix[s] = prefix;
+      prefix = prefix + s_slab_total[s];
+    }
+    s_slab_prefix[slabs] = prefix;
+    s_threshold = u[2 * depth + 1] * prefix;
+    s_candidate = INT_MAX;
+  }
+  __syncthreads();
+  const float threshold = s_threshold;
+  for (int base = 0; base < slabs; base += kWalkWaves) {
+    const int s = base + wave;
+    if (s < slabs) {
+      float e[32], incl[kLinesPerSlab], total[kLinesPerSlab];
+      const uint32_t bits = child_bits(s_child_tok, count, s, lane);
+      exit_values<kVec4>(x, a.vocab, m, s, lane, bits, e);
+      line_scans(e, lane, incl, total);
+      const float slab_prefix = s_slab_prefix[s];
+      int candidate = INT_MAX;
+      float lp = 0.0f;
+#pragma unroll
+      for (int j = 0; j < kLinesPerSlab; ++j) {
+        const float up = __shfl_up(incl[j], 1);
+        const float excl = (lane > 0) ? up : 0.0f;
+        float run = (slab_prefix + lp) + excl;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int t = s * kSlab + kLine * j + 4 * lane + c;
+          run = run + e[4 * j + c];
+          const bool hit = t < a.vocab && !((bits >> (4 * j + c)) & 1u) && run > threshold;
+          candidate = (hit && candidate == INT_MAX) ? t : candidate;
+        }
+        lp = lp + total[j];
+      }
+#pragma unroll
+      for (int d = 32; d >= 1; d >>= 1) candidate = min(candidate, __shfl_xor(candidate, d));
+      if (lane == 0 && candidate != INT_MAX) atomicMin(&s_candidate, candidate);
+    }
+    __syncthreads();
+    const int found = s_candidate;
+    __syncthreads();
+    if (found != INT_MAX) break;
+  }
+  if (tid == 0) {
+    int bonus = s_candidate;
+    if (bonus == INT_MAX) {
+      bonus = -1;
+      for (int t = a.vocab - 1; t >= 0; --t) {
+        bool child = false;
+        for (int k = 0; k < count; ++k) child = child || s_child_tok[k] == t;
+        if (!child) {
+          bonus = t;
+          break;
+        }
+      }
+    }
+    a.accept_len_dev[req] = depth;
+    a.bonus_dev[req] = bonus;
+  }
+  if (a.keep_rows_dev) {
+    int32_t* keep = a.keep_rows_dev + static_cast<int64_t>(a.max_depth + 1) * req;
+    for (int k = tid; k <= a.max_depth; k += kWalkThreads)
+      keep[k] = (k == 0) ? 0 : (k <= depth ? nodes_out[k - 1] : -1);
+  }
+}
+
+__global__ void exp_probe_kernel(const float* __restrict__ x, float* __restrict__ out,
+                                 int64_t count) {
+  const int64_t k = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (k < count) out[k] = sg_exp(x[k]);
+}
+
+bool vec4_ok(const float* p, int64_t stride, int vocab) {
+  return (reinterpret_cast<uintptr_t>(p) % 16 == 0) && stride % 4 == 0 && vocab % 4 == 0;
+}
+
+int launch_row_stats(const float* logits, int64_t stride, int vocab, int rows,
+                     float* row_max, float* row_sum, hipStream_t stream) {
+  if (rows == 0) return SG_OK;
+  const int rows_per_block = kStatsThreads / kWave;
+  const dim3 grid((rows + rows_per_block - 1) / rows_per_block);
+  if (vec4_ok(logits, stride, vocab)) {
+    hipLaunchKernelGGL(row_stats_kernel<true>, grid, dim3(kStatsThreads), 0, stream,
+                       logits, stride, vocab, rows, row_max, row_sum);
+  } else {
+    hipLaunchKernelGGL(row_stats_kernel<false>, grid, dim3(kStatsThreads), 0, stream,
+                       logits, stride, vocab, rows, row_max, row_sum);
+  }
+  SG_LAUNCH_CHECK();
+  return SG_OK;
+}
+
+}  // namespace
+}  // namespace sg
+
+extern "C" int sg_row_stats(const float* logits_dev, int64_t row_stride, int32_t vocab,
+                            int32_t num_rows, float* row_max_dev, float* row_sum_dev,
+                            sg_stream_t stream) {
+  using namespace sg;
+  clear_error();
+  SG_REQUIRE(vocab >= 1 && vocab <= kMaxSlabs * kSlab, "vocab must be in [1, 524288]");
+  SG_REQUIRE(num_rows >= 0, "num_rows must be non-negative");
+  SG_REQUIRE(row_stride >= vocab, "logits row stride is below the vocabulary");
+  SG_REQUIRE(num_rows == 0 || (logits_dev && row_max_dev && row_sum_dev),
+             "null device pointer");
+  return launch_row_stats(logits_dev, row_stride, vocab, num_rows, row_max_dev,
+                          row_sum_dev, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int sg_tree_sample(const SgTreeSampleArgs* args, sg_stream_t stream) {
+  using namespace sg;
+  clear_error();
+  SG_REQUIRE(args != nullptr, "null SgTreeSampleArgs");
+  const SgTreeSampleArgs& a = *args;
+  SG_REQUIRE(a.num_requests >= 0 && a.num_rows >= 0, "negative sizes");
+  SG_REQUIRE(a.vocab >= 1 && a.vocab <= kMaxSlabs * kSlab, "vocab must be in [1, 524288]");
+  SG_REQUIRE(a.logits_row_stride >= a.vocab, "logits row stride is below the vocabulary");
+  SG_REQUIRE(a.max_depth >= 0, "max_depth must be non-negative");
+  SG_REQUIRE(a.uniform_stride >= 2 * (a.max_depth + 1),
+             "uniform_stride must cover 2*(max_depth+1) uniforms");
+  if (a.num_requests == 0) return SG_OK;
+  SG_REQUIRE(a.logits_dev && a.row_offset_dev && a.parent_dev && a.token_dev &&
+                 a.uniforms_dev && a.row_max_dev && a.row_sum_dev && a.accept_len_dev &&
+                 a.bonus_dev && (a.max_depth == 0 || a.accept_nodes_dev),
+             "null device pointer");
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  int rc = launch_row_stats(a.logits_dev, a.logits_row_stride, a.vocab, a.num_rows,
+                            a.row_max_dev, a.row_sum_dev, s);
+  if (rc != SG_OK) return rc;
+  if (vec4_ok(a.logits_dev, a.logits_row_stride, a.vocab)) {
+    hipLaunchKernelGGL(tree_walk_kernel<true>, dim3(a.num_requests), dim3(kWalkThreads), 0,
+                       s, a);
+  } else {
+    hipLaunchKernelGGL(tree_walk_kernel<false>, dim3(a.num_requests), dim3(kWalkThreads), 0,
+                       s, a);
+  }
+  SG_LAUNCH_CHECK();
+  return SG_OK;
+}
+
+extern "C" int sg_exp_probe(const float* x_dev, float* out_dev, int64_t count,
+                            sg_stream_t stream) {
+  using namespace sg;
+  clear_error();
+  SG_REQUIRE(count >= 0, "negative count");
+  if (count == 0) return SG_OK;
+  SG_REQUIRE(x_dev && out_dev, "null device pointer");
+  const int threads = 256;
+  const dim3 grid(static_cast<unsigned>((count + threads - 1) / threads));
+  hipLaunchKernelGGL(exp_probe_kernel, grid, dim3(threads), 0,
+                     reinterpret_cast<hipStream_t>(stream), x_dev, out_dev, count);
+  SG_LAUNCH_CHECK();
+  return SG_OK;
+}

@@ -1,0 +1,327 @@
+"""Torch-facing wrappers of the HIP kernels (PyTorch is only the memory and
+stream plumbing here: tensors are passed to the C ABI as raw device pointers,
+and every call is enqueued on torch's current HIP stream).
+
+Argument checks follow the reference's native-op conventions
+(fused_tree_sampling.py:158-174, :472-509): contiguity/device/dtype problems
+raise ValueError before anything is launched; launch errors raise RuntimeError.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _lib
+
+
+def _stream_handle() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _require(cond: bool, message: str) -> None:
+    if not cond:
+        raise ValueError(message)
+
+
+def _check_device_tensor(t: torch.Tensor, name: str, dtype: torch.dtype) -> None:
+    _require(isinstance(t, torch.Tensor), f"{name} must be a tensor")
+    _require(t.is_cuda, f"{name} must be a HIP device tensor")
+    _require(t.dtype == dtype, f"{name} must be {dtype}, got {t.dtype}")
+
+
+def _check_rows(t: torch.Tensor, name: str) -> None:
+    """bf16 tensors whose last (head) dim is contiguous and 16-byte aligned."""
+    _check_device_tensor(t, name, torch.bfloat16)
+    _require(t.stride(-1) == 1, f"{name} must have a contiguous last dimension")
+    _require(t.data_ptr() % 16 == 0, f"{name} must be 16-byte aligned")
+    for s in t.stride()[:-1]:
+        _require(s % 8 == 0, f"{name} strides must be multiples of 8 elements")
+
+
+# --------------------------------------------------------------------------
+# (A) attention
+# --------------------------------------------------------------------------
+
+@dataclass
+class AttnPlan:
+    """Host-built work list of the packed attention (one per wave, all layers)."""
+    host: np.ndarray
+    units: int
+    merges: int
+    workspace_bytes: int
+    num_q_heads: int
+    num_kv_heads: int
+    head_dim: int
+    device: torch.Tensor | None = None
+    workspace: torch.Tensor | None = None
+
+    def to(self, device) -> "AttnPlan":
+        self.device = torch.from_numpy(self.host).to(device, non_blocking=False)
+        self.workspace = torch.empty(max(self.workspace_bytes, 16), dtype=torch.uint8,
+                                     device=device)
+        return self
+
+
+def plan_attention(row_offset, prefix_len, num_q_heads: int, num_kv_heads: int,
+                   head_dim: int, target_units: int = 0) -> AttnPlan:
+    lib = _lib.load()
+    ro = np.ascontiguousarray(np.asarray(row_offset, dtype=np.int32))
+    pl = np.ascontiguousarray(np.asarray(prefix_len, dtype=np.int32))
+    n = int(pl.size)
+    _require(ro.size == n + 1, "row_offset must have num_requests + 1 entries")
+    i32p = ctypes.POINTER(ctypes.c_int32)
+    plan_bytes = ctypes.c_size_t()
+    units = ctypes.c_int32()
+    merges = ctypes.c_int32()
+    ws = ctypes.c_size_t()
+    args = (n, ro.ctypes.data_as(i32p), pl.ctypes.data_as(i32p), num_q_heads,
+            num_kv_heads, head_dim, target_units)
+    _lib.check(lib.sg_tree_attn_plan(*args, None, 0, ctypes.byref(plan_bytes),
+                                     ctypes.byref(units), ctypes.byref(merges),
+                                     ctypes.byref(ws)), "sg_tree_attn_plan")
+    host = np.zeros(plan_bytes.value, dtype=np.uint8)
+    _lib.check(lib.sg_tree_attn_plan(*args, host.ctypes.data_as(ctypes.c_void_p),
+                                     host.nbytes, ctypes.byref(plan_bytes),
+                                     ctypes.byref(units), ctypes.byref(merges),
+                                     ctypes.byref(ws)), "sg_tree_attn_plan")
+    return AttnPlan(host, units.value, merges.value, ws.value, num_q_heads,
+                    num_kv_heads, head_dim)
+
+
+def decode_plan(plan: AttnPlan):
+    """(header, units [U, 8], merges [M, 8]) int32 views of a host plan."""
+    words = plan.host.view(np.int32)
+    header = words[:16]
+    units = words[16:16 + 8 * plan.units].reshape(plan.units, 8)
+    merges = words[16 + 8 * plan.units:16 + 8 * (plan.units + plan.merges)].reshape(
+        plan.merges, 8)
+    return header, units, merges
+
+
+def tree_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                   k_tree: torch.Tensor, v_tree: torch.Tensor,
+                   row_offset: torch.Tensor, prefix_start: torch.Tensor,
+                   prefix_len: torch.Tensor, parent: torch.Tensor, plan: AttnPlan,
+                   out: torch.Tensor | None = None, scale: float | None = None,
+                   ) -> torch.Tensor:
+    """Packed tree attention of one layer.
+
+    q [R, Hq, D], k/v_cache [Hkv, tokens, D] (the cache arena of this layer),
+    k/v_tree [R, Hkv, D] (this wave's rows), row_offset [n+1] i32,
+    prefix_start [n] i64, prefix_len [n] i32, parent [R] i32.  Returns
+    out [R, Hq, D] bf16.
+    """
+    for t, name in ((q, "q"), (k_cache, "k_cache"), (v_cache, "v_cache"),
+                    (k_tree, "k_tree"), (v_tree, "v_tree")):
+        _check_rows(t, name)
+    _check_device_tensor(row_offset, "row_offset", torch.int32)
+    _check_device_tensor(prefix_start, "prefix_start", torch.int64)
+    _check_device_tensor(prefix_len, "prefix_len", torch.int32)
+    _check_device_tensor(parent, "parent", torch.int32)
+    _require(q.dim() == 3 and k_tree.dim() == 3 and k_cache.dim() == 3,
+             "q/k_tree must be [R, H, D] and k_cache [Hkv, tokens, D]")
+    rows, hq, dim = q.shape
+    hkv = k_cache.shape[0]
+    _require(k_cache.shape == v_cache.shape and k_cache.stride() == v_cache.stride(),
+             "k_cache and v_cache must share shape and strides")
+    _require(k_tree.shape == (rows, hkv, dim) and v_tree.shape == k_tree.shape
+             and k_tree.stride() == v_tree.stride(),
+             "k_tree/v_tree must be [R, Hkv, D] with equal strides")
+    _require(k_cache.shape[2] == dim, "head dims disagree")
+    _require((plan.num_q_heads, plan.num_kv_heads, plan.head_dim) == (hq, hkv, dim),
+             "plan was built for another head configuration")
+    _require(plan.device is not None and plan.device.is_cuda, "plan is not on the device")
+    _require(parent.numel() >= rows, "parent must cover every packed row")
+    n = prefix_len.numel()
+    _require(row_offset.numel() == n + 1 and prefix_start.numel() == n,
+             "request metadata sizes disagree")
+    if out is None:
+        out = torch.empty((rows, hq, dim), dtype=torch.bfloat16, device=q.device)
+    _check_rows(out, "out")
+    _require(out.shape == (rows, hq, dim), "out must be [R, Hq, D]")
+    a = _lib.SgTreeAttnArgs()
+    a.num_requests = n
+    a.num_rows = rows
+    a.num_q_heads = hq
+    a.num_kv_heads = hkv
+    a.head_dim = dim
+    a.scale = float(dim ** -0.5 if scale is None else scale)
+    a.q_dev = q.data_ptr()
+    a.q_row_stride, a.q_head_stride = q.stride(0), q.stride(1)
+    a.k_cache_dev = k_cache.data_ptr()
+    a.v_cache_dev = v_cache.data_ptr()
+    a.cache_head_stride, a.cache_token_stride = k_cache.stride(0), k_cache.stride(1)
+    a.k_tree_dev = k_tree.data_ptr()
+    a.v_tree_dev = v_tree.data_ptr()
+    a.tree_row_stride, a.tree_head_stride = k_tree.stride(0), k_tree.stride(1)
+    a.row_offset_dev = row_offset.data_ptr()
+    a.prefix_start_dev = prefix_start.data_ptr()
+    a.prefix_len_dev = prefix_len.data_ptr()
+    a.parent_dev = parent.data_ptr()
+    a.out_dev = out.data_ptr()
+    a.out_row_stride, a.out_head_stride = out.stride(0), out.stride(1)
+    a.plan_dev = plan.device.data_ptr()
+    a.plan_units = plan.units
+    a.plan_merges = plan.merges
+    a.workspace_dev = plan.workspace.data_ptr() if plan.workspace is not None else 0
+    a.workspace_bytes = plan.workspace.numel() if plan.workspace is not None else 0
+    _lib.check(_lib.load().sg_tree_attn_fwd(ctypes.byref(a), _stream_handle()),
+               "sg_tree_attn_fwd")
+    return out
+
+
+# --------------------------------------------------------------------------
+# (B) KV commit
+# --------------------------------------------------------------------------
+
+def pointer_array(tensors, device) -> torch.Tensor:
+    """Device array of the tensors' base addresses (int64)."""
+    return torch.tensor([t.data_ptr() for t in tensors], dtype=torch.int64, device=device)
+
+
+def kv_commit(k_cache_ptrs: torch.Tensor, v_cache_ptrs: torch.Tensor,
+              k_tree_ptrs: torch.Tensor, v_tree_ptrs: torch.Tensor, *,
+              num_kv_heads: int, head_dim: int, cache_head_stride: int,
+              cache_token_stride: int, tree_row_stride: int, tree_head_stride: int,
+              row_offset: torch.Tensor, keep_rows: torch.Tensor, keep_len: torch.Tensor,
+              prefix_start: torch.Tensor, lengths: torch.Tensor, capacity: int,
+              status: torch.Tensor | None = None) -> None:
+    """Scatter the kept rows of every layer into the cache (one launch).
+
+    ``*_ptrs`` are int64 device arrays of per-layer base addresses (see
+    pointer_array); keep_rows [n, keep_stride] i32, keep_len [n] i32,
+    prefix_start [n] i64, lengths [n] i32 (advanced in place).
+    """
+    for t, name in ((k_cache_ptrs, "k_cache_ptrs"), (v_cache_ptrs, "v_cache_ptrs"),
+                    (k_tree_ptrs, "k_tree_ptrs"), (v_tree_ptrs, "v_tree_ptrs"),
+                    (prefix_start, "prefix_start")):
+        _check_device_tensor(t, name, torch.int64)
+    for t, name in ((row_offset, "row_offset"), (keep_rows, "keep_rows"),
+                    (keep_len, "keep_len"), (lengths, "lengths")):
+        _check_device_tensor(t, name, torch.int32)
+    layers = k_cache_ptrs.numel()
+    _require(v_cache_ptrs.numel() == layers and k_tree_ptrs.numel() == layers
+             and v_tree_ptrs.numel() == layers, "per-layer pointer arrays disagree")
+    _require(keep_rows.dim() == 2 and keep_rows.is_contiguous(), "keep_rows must be [n, stride]")
+    n = keep_rows.shape[0]
+    _require(keep_len.numel() == n and lengths.numel() == n and prefix_start.numel() == n
+             and row_offset.numel() == n + 1, "request metadata sizes disagree")
+    if status is not None:
+        _check_device_tensor(status, "status", torch.int32)
+    a = _lib.SgKvCommitArgs()
+    a.num_layers = layers
+    a.num_requests = n
+    a.num_kv_heads = num_kv_heads
+    a.head_dim = head_dim
+    a.k_cache_layers_dev = k_cache_ptrs.data_ptr()
+    a.v_cache_layers_dev = v_cache_ptrs.data_ptr()
+    a.cache_head_stride = cache_head_stride
+    a.cache_token_stride = cache_token_stride
+    a.k_tree_layers_dev = k_tree_ptrs.data_ptr()
+    a.v_tree_layers_dev = v_tree_ptrs.data_ptr()
+    a.tree_row_stride = tree_row_stride
+    a.tree_head_stride = tree_head_stride
+    a.row_offset_dev = row_offset.data_ptr()
+    a.keep_rows_dev = keep_rows.data_ptr()
+    a.keep_stride = keep_rows.shape[1]
+    a.keep_len_dev = keep_len.data_ptr()
+    a.prefix_start_dev = prefix_start.data_ptr()
+    a.lengths_dev = lengths.data_ptr()
+    a.capacity = capacity
+    a.status_dev = status.data_ptr() if status is not None else 0
+    _lib.check(_lib.load().sg_kv_commit(ctypes.byref(a), _stream_handle()), "sg_kv_commit")
+
+
+# --------------------------------------------------------------------------
+# (C) tree sampling
+# --------------------------------------------------------------------------
+
+@dataclass
+class SampleResult:
+    accept_nodes: torch.Tensor  # [n, max_depth] i32, -1 padded
+    accept_len: torch.Tensor    # [n] i32
+    bonus: torch.Tensor         # [n] i32
+    keep_rows: torch.Tensor     # [n, max_depth + 1] i32 ([0] + nodes, -1 padded)
+    row_max: torch.Tensor       # [R] f32
+    row_sum: torch.Tensor       # [R] f32
+    status: torch.Tensor        # [1] i32
+
+
+def tree_sample(logits: torch.Tensor, row_offset: torch.Tensor, parent: torch.Tensor,
+                token: torch.Tensor, uniforms: torch.Tensor, max_depth: int,
+                out: SampleResult | None = None) -> SampleResult:
+    """Temperature-1 tree rejection sampling over all packed rows.
+
+    logits [R, V] fp32 (row-contiguous), row_offset [n+1] i32, parent/token
+    [R] i32 (request-local parents, -1 for roots), uniforms [n, U] fp32 with
+    U >= 2*(max_depth+1).
+    """
+    _check_device_tensor(logits, "logits", torch.float32)
+    _require(logits.dim() == 2 and logits.stride(1) == 1, "logits must be [R, V] row-contiguous")
+    for t, name in ((row_offset, "row_offset"), (parent, "parent"), (token, "token")):
+        _check_device_tensor(t, name, torch.int32)
+        _require(t.is_contiguous(), f"{name} must be contiguous")
+    _check_device_tensor(uniforms, "uniforms", torch.float32)
+    _require(uniforms.dim() == 2 and uniforms.is_contiguous(), "uniforms must be [n, U]")
+    n = row_offset.numel() - 1
+    rows = logits.shape[0]
+    _require(uniforms.shape[0] == n, "one uniform row per request")
+    _require(uniforms.shape[1] >= 2 * (max_depth + 1), "uniforms must cover 2*(max_depth+1)")
+    _require(parent.numel() >= rows and token.numel() >= rows, "parent/token must cover R rows")
+    dev = logits.device
+    if out is None:
+        depth_slots = max(max_depth, 1)
+        out = SampleResult(
+            accept_nodes=torch.empty((n, depth_slots), dtype=torch.int32, device=dev),
+            accept_len=torch.empty(n, dtype=torch.int32, device=dev),
+            bonus=torch.empty(n, dtype=torch.int32, device=dev),
+            keep_rows=torch.empty((n, max_depth + 1), dtype=torch.int32, device=dev),
+            row_max=torch.empty(rows, dtype=torch.float32, device=dev),
+            row_sum=torch.empty(rows, dtype=torch.float32, device=dev),
+            status=torch.zeros(1, dtype=torch.int32, device=dev),
+        )
+    a = _lib.SgTreeSampleArgs()
+    a.num_requests = n
+    a.num_rows = rows
+    a.vocab = logits.shape[1]
+    a.max_depth = max_depth
+    a.logits_dev = logits.data_ptr()
+    a.logits_row_stride = logits.stride(0)
+    a.row_offset_dev = row_offset.data_ptr()
+    a.parent_dev = parent.data_ptr()
+    a.token_dev = token.data_ptr()
+    a.uniforms_dev = uniforms.data_ptr()
+    a.uniform_stride = uniforms.shape[1]
+    a.row_max_dev = out.row_max.data_ptr()
+    a.row_sum_dev = out.row_sum.data_ptr()
+    a.accept_nodes_dev = out.accept_nodes.data_ptr()
+    a.accept_len_dev = out.accept_len.data_ptr()
+    a.bonus_dev = out.bonus.data_ptr()
+    a.keep_rows_dev = out.keep_rows.data_ptr()
+    a.status_dev = out.status.data_ptr()
+    _lib.check(_lib.load().sg_tree_sample(ctypes.byref(a), _stream_handle()), "sg_tree_sample")
+    return out
+
+
+def row_stats(logits: torch.Tensor):
+    _check_device_tensor(logits, "logits", torch.float32)
+    _require(logits.dim() == 2 and logits.stride(1) == 1, "logits must be [R, V] row-contiguous")
+    rows = logits.shape[0]
+    m = torch.empty(rows, dtype=torch.float32, device=logits.device)
+    z = torch.empty(rows, dtype=torch.float32, device=logits.device)
+    _lib.check(_lib.load().sg_row_stats(logits.data_ptr(), logits.stride(0), logits.shape[1],
+                                        rows, m.data_ptr(), z.data_ptr(), _stream_handle()),
+               "sg_row_stats")
+    return m, z
+
+
+def exp_probe(x: torch.Tensor) -> torch.Tensor:
+    _check_device_tensor(x, "x", torch.float32)
+    x = x.contiguous()
+    out = torch.empty_like(x)
+    _lib.check(_lib.load().sg_exp_probe(x.data_ptr(), out.data_ptr(), x.numel(),
+                                        _stream_handle()), "sg_exp_probe")
+    return out

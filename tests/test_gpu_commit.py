@@ -1,0 +1,113 @@
+"""GPU parity of the accepted-path KV commit against the CPU oracle: bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+from specgrove_amd import ops
+from specgrove_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+
+def _commit_case(device, oracle, wl, layers, seed, lengths=None):
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    n = wl.num_requests
+    hkv, d = wl.num_kv_heads, wl.head_dim
+    rows = wl.total_rows
+    cache_k = torch.randn((layers, hkv, n * wl.capacity, d), generator=gen).to(torch.bfloat16)
+    cache_v = torch.randn((layers, hkv, n * wl.capacity, d), generator=gen).to(torch.bfloat16)
+    tree_k = torch.randn((layers, rows, hkv, d), generator=gen).to(torch.bfloat16)
+    tree_v = torch.randn((layers, rows, hkv, d), generator=gen).to(torch.bfloat16)
+    if lengths is None:
+        lengths = wl.prefix_len.astype(np.int32)
+    keep_stride = max(len(k) for k in wl.keep)
+    keep = np.full((n, keep_stride), -1, np.int32)
+    for i, k in enumerate(wl.keep):
+        keep[i, :len(k)] = k
+    keep_len = np.asarray([len(k) for k in wl.keep], np.int32)
+
+    dk, dv = cache_k.to(device), cache_v.to(device)
+    tk, tv = tree_k.to(device), tree_v.to(device)
+    lengths_dev = torch.from_numpy(lengths.copy()).to(device)
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    ops.kv_commit(
+        ops.pointer_array([dk[l] for l in range(layers)], device),
+        ops.pointer_array([dv[l] for l in range(layers)], device),
+        ops.pointer_array([tk[l] for l in range(layers)], device),
+        ops.pointer_array([tv[l] for l in range(layers)], device),
+        num_kv_heads=hkv, head_dim=d, cache_head_stride=dk.stride(1),
+        cache_token_stride=dk.stride(2), tree_row_stride=tk.stride(1),
+        tree_head_stride=tk.stride(2),
+        row_offset=torch.from_numpy(wl.row_offset).to(device),
+        keep_rows=torch.from_numpy(keep).to(device),
+        keep_len=torch.from_numpy(keep_len).to(device),
+        prefix_start=torch.from_numpy(wl.prefix_start).to(device),
+        lengths=lengths_dev, capacity=wl.capacity, status=status)
+    torch.cuda.synchronize()
+
+    ok = cache_k.view(torch.int16).numpy().copy()
+    ov = cache_v.view(torch.int16).numpy().copy()
+    olen = lengths.copy()
+    oracle.kv_commit(ok, ov, olen, wl.capacity, range(n),
+                     tree_k.view(torch.int16).numpy(), tree_v.view(torch.int16).numpy(),
+                     wl.row_offset, wl.keep)
+    return dk, dv, lengths_dev, status, ok, ov, olen
+
+
+def test_commit_qwen3_8b_shape_bit_exact(device, oracle):
+    wl = W.qwen3_8b_workload()
+    dk, dv, lengths_dev, status, ok, ov, olen = _commit_case(device, oracle, wl, 2, 0)
+    assert int(status.item()) == 0
+    np.testing.assert_array_equal(lengths_dev.cpu().numpy(), olen)
+    assert np.array_equal(dk.cpu().view(torch.int16).numpy(), ok)
+    assert np.array_equal(dv.cpu().view(torch.int16).numpy(), ov)
+
+
+def test_commit_tiny_many_layers_bit_exact(device, oracle):
+    wl = W.tiny_attention_workload(seed=5)
+    dk, dv, lengths_dev, status, ok, ov, olen = _commit_case(device, oracle, wl, 5, 1)
+    assert int(status.item()) == 0
+    np.testing.assert_array_equal(lengths_dev.cpu().numpy(), olen)
+    assert np.array_equal(dk.cpu().view(torch.int16).numpy(), ok)
+    assert np.array_equal(dv.cpu().view(torch.int16).numpy(), ov)
+
+
+def test_commit_capacity_overflow_reports_erange(device, oracle):
+    wl = W.tiny_attention_workload(seed=6)
+    lengths = wl.prefix_len.astype(np.int32).copy()
+    lengths[1] = wl.capacity - 1          # request 1 cannot take its kept rows
+    gen = torch.Generator(device="cpu").manual_seed(3)
+    n, hkv, d = wl.num_requests, wl.num_kv_heads, wl.head_dim
+    cache = torch.randn((hkv, n * wl.capacity, d), generator=gen).to(torch.bfloat16).to(device)
+    before = cache.clone()
+    tree = torch.randn((wl.total_rows, hkv, d), generator=gen).to(torch.bfloat16).to(device)
+    keep = np.full((n, 16), -1, np.int32)
+    for i, k in enumerate(wl.keep):
+        keep[i, :len(k)] = k
+    keep_len = np.asarray([len(k) for k in wl.keep], np.int32)
+    lengths_dev = torch.from_numpy(lengths.copy()).to(device)
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    ptr = ops.pointer_array([cache], device)
+    tptr = ops.pointer_array([tree], device)
+    ops.kv_commit(ptr, ptr, tptr, tptr, num_kv_heads=hkv, head_dim=d,
+                  cache_head_stride=cache.stride(0), cache_token_stride=cache.stride(1),
+                  tree_row_stride=tree.stride(0), tree_head_stride=tree.stride(1),
+                  row_offset=torch.from_numpy(wl.row_offset).to(device),
+                  keep_rows=torch.from_numpy(keep).to(device),
+                  keep_len=torch.from_numpy(keep_len).to(device),
+                  prefix_start=torch.from_numpy(wl.prefix_start).to(device),
+                  lengths=lengths_dev, capacity=wl.capacity, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == -2
+    got = lengths_dev.cpu().numpy()
+    assert got[1] == lengths[1]
+    expected = lengths + keep_len
+    expected[1] = lengths[1]
+    np.testing.assert_array_equal(got, expected)
+    region = slice(wl.capacity, 2 * wl.capacity)
+    assert torch.equal(cache[:, region], before[:, region])
+    with pytest.raises(RuntimeError, match="capacity exhausted"):
+        oracle.kv_commit(np.zeros((1, hkv, n * wl.capacity, d)),
+                         np.zeros((1, hkv, n * wl.capacity, d)), lengths.copy(),
+                         wl.capacity, range(n), np.zeros((1, wl.total_rows, hkv, d)),
+                         np.zeros((1, wl.total_rows, hkv, d)), wl.row_offset, wl.keep)

@@ -1,0 +1,128 @@
+"""GPU parity of the tree sampler against the CPU oracle: bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+from specgrove_amd import ops
+from specgrove_amd import workloads as W
+from tests.sampler_cases import tree_problem
+
+pytestmark = pytest.mark.gpu
+
+
+def _run_gpu(case, device):
+    t = {k: torch.from_numpy(case[k]).to(device)
+         for k in ("logits", "row_offset", "parent", "token", "uniforms")}
+    res = ops.tree_sample(t["logits"], t["row_offset"], t["parent"], t["token"],
+                          t["uniforms"], case["max_depth"])
+    torch.cuda.synchronize()
+    return {k: getattr(res, k).cpu().numpy() for k in
+            ("accept_nodes", "accept_len", "bonus", "keep_rows", "row_max", "row_sum", "status")}
+
+
+def _check_case(case, device, oracle):
+    gpu = _run_gpu(case, device)
+    nodes, length, bonus, m, z = oracle.tree_sample(
+        case["logits"], case["row_offset"], case["parent"], case["token"],
+        case["uniforms"], case["max_depth"])
+    assert gpu["status"][0] == 0
+    np.testing.assert_array_equal(gpu["row_max"], m)
+    assert np.array_equal(gpu["row_sum"].view(np.uint32), z.view(np.uint32)), \
+        "row sums differ in bits"
+    np.testing.assert_array_equal(gpu["accept_len"], length)
+    np.testing.assert_array_equal(gpu["accept_nodes"][:, :case["max_depth"]], nodes)
+    np.testing.assert_array_equal(gpu["bonus"], bonus)
+    keep = np.full((len(length), case["max_depth"] + 1), -1, np.int32)
+    keep[:, 0] = 0
+    for i, a in enumerate(length):
+        keep[i, 1:1 + a] = nodes[i, :a]
+    np.testing.assert_array_equal(gpu["keep_rows"], keep)
+    return gpu
+
+
+def test_exp_bit_exact(device, oracle):
+    xs = np.concatenate([
+        np.linspace(-90, 1, 200001, dtype=np.float32),
+        np.array([0.0, -0.0, -87.0, np.nextafter(np.float32(-87.0), np.float32(0)),
+                  np.nextafter(np.float32(-87.0), np.float32(-100)), -1e-30, 1e-30,
+                  -np.inf, np.nan, 88.0, 89.0], np.float32),
+        -np.abs(np.random.default_rng(0).standard_normal(100000).astype(np.float32) * 30),
+    ])
+    got = ops.exp_probe(torch.from_numpy(xs).to(device)).cpu().numpy()
+    want = oracle.exp_f32(xs)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("vocab", [1, 3, 100, 2048, 2049, 4096, 4097, 151936])
+def test_row_stats_bit_exact(device, oracle, vocab):
+    rng = np.random.default_rng(vocab)
+    rows = 9
+    x = (rng.standard_normal((rows, vocab)) * 4).astype(np.float32)
+    x[1] -= 200.0                      # deep negative row
+    x[2, ::7] = -np.inf                # masked tokens
+    x[3, :] = 5.0                      # constant row
+    m, z = ops.row_stats(torch.from_numpy(x).to(device))
+    m, z = m.cpu().numpy(), z.cpu().numpy()
+    for r in range(rows):
+        om, oz = oracle.row_stats(x[r])
+        assert m[r] == om
+        assert np.float32(z[r]).view(np.uint32) == np.float32(oz).view(np.uint32), (r, z[r], oz)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2, 3])
+def test_tiny_vocab_trees_bit_exact(device, oracle, seed):
+    case = tree_problem(seed, num_requests=6, nodes=[16, 1, 9, 16, 3, 12], vocab=4096)
+    _check_case(case, device, oracle)
+
+
+@pytest.mark.parametrize("vocab,nodes", [(2, [2, 2, 1, 2, 2]), (5, [2, 3, 4, 1, 2]),
+                                         (4097, [12, 12, 12, 12, 12])])
+def test_odd_vocab_bit_exact(device, oracle, vocab, nodes):
+    case = tree_problem(10 + vocab, num_requests=5, nodes=nodes, vocab=vocab, child_boost=2.0)
+    _check_case(case, device, oracle)
+
+
+def test_extreme_uniforms_bit_exact(device, oracle):
+    case = tree_problem(7, num_requests=9, nodes=16, vocab=4096, extreme_uniforms=True)
+    gpu = _check_case(case, device, oracle)
+    assert (gpu["accept_len"][0::3] >= 1).any()
+
+
+def test_qwen_vocab_bit_exact(device, oracle):
+    case = tree_problem(11, num_requests=8, nodes=32, vocab=151936, random_trees=False)
+    gpu = _check_case(case, device, oracle)
+    assert gpu["accept_len"].max() >= 1
+
+
+def test_golden_fixture(device):
+    from pathlib import Path
+    path = Path(__file__).parent / "golden" / "sampler_tiny.npz"
+    data = np.load(path, allow_pickle=False)
+    case = {k: data[k] for k in ("logits", "row_offset", "parent", "token", "uniforms")}
+    case["max_depth"] = int(data["max_depth"])
+    gpu = _run_gpu(case, device)
+    np.testing.assert_array_equal(gpu["accept_len"], data["accept_len"])
+    np.testing.assert_array_equal(gpu["accept_nodes"], data["accept_nodes"])
+    np.testing.assert_array_equal(gpu["bonus"], data["bonus"])
+
+
+def test_sampler_workload_full_size(device, oracle):
+    """64 requests x 32 nodes, vocab 151936: every request bit-exact."""
+    wl, logits, uniforms = W.sampler_workload(device)
+    parent, token = wl.flat_parent_token()
+    case = dict(logits=logits.cpu().numpy(), row_offset=wl.row_offset, parent=parent,
+                token=token, uniforms=uniforms.cpu().numpy(), max_depth=wl.max_depth)
+    gpu = _check_case(case, device, oracle)
+    assert gpu["accept_len"].mean() > 0.5
+
+
+def test_invalid_arguments_raise(device):
+    logits = torch.zeros((4, 16), device=device)
+    ro = torch.tensor([0, 4], dtype=torch.int32, device=device)
+    par = torch.tensor([-1, 0, 0, 1], dtype=torch.int32, device=device)
+    tok = torch.tensor([0, 1, 2, 3], dtype=torch.int32, device=device)
+    u = torch.zeros((1, 2), device=device)
+    with pytest.raises(ValueError):
+        ops.tree_sample(logits, ro, par, tok, u, max_depth=2)
+    with pytest.raises(ValueError):
+        ops.tree_sample(logits.double(), ro, par, tok, torch.zeros((1, 6), device=device), 2)
