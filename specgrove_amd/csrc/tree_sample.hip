@@ -288,7 +288,12 @@ __global__ __launch_bounds__(kWalkThreads) void tree_walk_kernel(SgTreeSampleArg
         const float threshold = u[2 * depth] * a.row_sum_dev[row];
         float cumulative = 0.0f;
         for (int k = 0; k < s_child_count; ++k) {
-          cumulative = cumulative + sg_exp(x[s_child_tok[k]] - m);
+          const int tok = s_child_tok[k];
+          if (tok < 0 || tok >= a.vocab) {
+            accepted = -2;  // draft token outside the vocabulary
+            break;
+          }
+          cumulative = cumulative + sg_exp(x[tok] - m);
           if (threshold < cumulative) {
             accepted = s_child_node[k];
             break;
