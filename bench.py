@@ -1,0 +1,315 @@
+"""Benchmark of the packed target-verification path on one MI355X.
+
+Step (the unit timed K times): one packed verification wave at the Qwen3-8B
+attention shape -- 64 requests, 2048 packed rows, prefixes U{512..4096},
+32 q / 8 kv heads, D 128, bf16 -- i.e. the request-isolated tree attention of
+one layer followed by the accepted-path KV commit of 1 + a_i rows per request.
+value = packed rows / step time.  Inputs are resident in HBM; three distinct
+input sets (each with its own >1 GB KV cache) rotate so the 256 MB
+Infinity Cache cannot serve repeated reads.
+
+Also reported in the same JSON line:
+  attention   per-call time of sg_tree_attn_fwd (HIP events on the launch stream),
+              rows/s, algorithmic GB/s and the fraction of 8 TB/s (= "roofline");
+  commit      per-call time of sg_kv_commit;
+  sampler     tree sampling over 64 x 32 nodes, vocab 151936 (nodes/s, GB/s);
+  cpu_baseline the reference's CPU path restated (dense packed mask + SDPA in
+              fp32) on a bounded sample, timed on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+N_SETS = 3
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-sampler", action="store_true")
+    p.add_argument("--cpu-requests", type=int, default=16,
+                   help="requests in the CPU baseline's dense packed sample")
+    p.add_argument("--target-units", type=int, default=0)
+    return p.parse_args()
+
+
+def _events(torch, n):
+    return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+
+
+def time_calls(torch, fn, iters):
+    """Per-call milliseconds from HIP events recorded on the current stream."""
+    starts, ends = _events(torch, iters), _events(torch, iters)
+    for k in range(iters):
+        starts[k].record()
+        fn(k)
+        ends[k].record()
+    torch.cuda.synchronize()
+    return [s.elapsed_time(e) for s, e in zip(starts, ends)]
+
+
+def build_attention_sets(torch, np, W, ops, device, steps_total):
+    wl = W.qwen3_8b_workload()
+    # headroom so every timed commit appends inside the slot
+    max_keep = max(len(k) for k in wl.keep)
+    wl.capacity = (int(wl.prefix_len.max()) + 128 + max_keep * (steps_total + 2) + 63) // 64 * 64
+    plan = ops.plan_attention(wl.row_offset, wl.prefix_len, wl.num_q_heads, wl.num_kv_heads,
+                              wl.head_dim, 0).to(device)
+    meta = dict(
+        row_offset=torch.from_numpy(wl.row_offset).to(device),
+        prefix_start=torch.from_numpy(wl.prefix_start).to(device),
+        prefix_len=torch.from_numpy(wl.prefix_len.astype(np.int32)).to(device),
+        parent=torch.from_numpy(wl.parent_flat).to(device),
+    )
+    keep_stride = max_keep
+    keep = np.full((wl.num_requests, keep_stride), -1, np.int32)
+    for i, k in enumerate(wl.keep):
+        keep[i, :len(k)] = k
+    meta["keep_rows"] = torch.from_numpy(keep).to(device)
+    meta["keep_len"] = torch.from_numpy(
+        np.asarray([len(k) for k in wl.keep], np.int32)).to(device)
+    sets = []
+    for s in range(N_SETS):
+        q, kc, vc, kt, vt = wl.make_tensors(device, seed=100 + s)
+        out = torch.empty_like(q)
+        lengths = meta["prefix_len"].clone()
+        ptrs = [ops.pointer_array([t], device) for t in (kc, vc, kt, vt)]
+        sets.append(dict(q=q, kc=kc, vc=vc, kt=kt, vt=vt, out=out, lengths=lengths,
+                         ptrs=ptrs))
+    return wl, plan, meta, sets
+
+
+def attention_call(ops, wl, plan, meta, st):
+    ops.tree_attention(st["q"], st["kc"], st["vc"], st["kt"], st["vt"], meta["row_offset"],
+                       meta["prefix_start"], meta["prefix_len"], meta["parent"], plan,
+                       out=st["out"])
+
+
+def commit_call(ops, wl, meta, st):
+    kc = st["kc"]
+    kt = st["kt"]
+    ops.kv_commit(*st["ptrs"], num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim,
+                  cache_head_stride=kc.stride(0), cache_token_stride=kc.stride(1),
+                  tree_row_stride=kt.stride(0), tree_head_stride=kt.stride(1),
+                  row_offset=meta["row_offset"], keep_rows=meta["keep_rows"],
+                  keep_len=meta["keep_len"], prefix_start=meta["prefix_start"],
+                  lengths=st["lengths"], capacity=wl.capacity)
+
+
+def sampler_bench(torch, W, ops, device, iters, warmup):
+    sets = []
+    for s in range(N_SETS):
+        wl, logits, uniforms = W.sampler_workload(device, seed=200 + s)
+        parent, token = wl.flat_parent_token()
+        sets.append(dict(wl=wl, logits=logits, uniforms=uniforms,
+                         row_offset=torch.from_numpy(wl.row_offset).to(device),
+                         parent=torch.from_numpy(parent).to(device),
+                         token=torch.from_numpy(token).to(device)))
+    results = [None] * N_SETS
+
+    def call(k):
+        st = sets[k % N_SETS]
+        results[k % N_SETS] = ops.tree_sample(st["logits"], st["row_offset"], st["parent"],
+                                              st["token"], st["uniforms"], st["wl"].max_depth,
+                                              out=results[k % N_SETS])
+
+    for k in range(warmup):
+        call(k)
+    torch.cuda.synchronize()
+    ms = time_calls(torch, call, iters)
+    wl = sets[0]["wl"]
+    return wl, ms, sets
+
+
+def cpu_attention_baseline(torch, np, W, requests):
+    """Reference wave restated on the CPU: dense packed mask + fp32 SDPA."""
+    from oracle import oracle
+    threads = oracle.cpu_threads()
+    torch.set_num_threads(threads)
+    wl = W.qwen3_8b_workload()
+    sub = list(range(requests))
+    q, kc, vc, kt, vt = wl.make_tensors("cpu", seed=100)
+    rows = wl.row_offset
+    q_sub = torch.cat([q[rows[i]:rows[i + 1]] for i in sub])
+    kt_sub = torch.cat([kt[rows[i]:rows[i + 1]] for i in sub])
+    vt_sub = torch.cat([vt[rows[i]:rows[i + 1]] for i in sub])
+    ks = [kc[:, int(wl.prefix_start[i]):int(wl.prefix_start[i]) + int(wl.prefix_len[i])]
+          for i in sub]
+    vs = [vc[:, int(wl.prefix_start[i]):int(wl.prefix_start[i]) + int(wl.prefix_len[i])]
+          for i in sub]
+    parents = [wl.parents[i] for i in sub]
+    t0 = time.perf_counter()
+    oracle.attention_dense(q_sub, ks, vs, kt_sub, vt_sub, parents)
+    elapsed = time.perf_counter() - t0
+    n_rows = int(q_sub.shape[0])
+    return dict(value=n_rows / elapsed, unit="rows/s", cores=threads, kind="port",
+                sample=(f"dense packed wave of the first {requests} of 64 requests "
+                        f"({n_rows} rows, {int(sum(wl.prefix_len[:requests]))} prefix keys), "
+                        f"fp32 torch SDPA with additive mask and repeat_kv, "
+                        f"{elapsed:.2f} s on {platform.processor() or platform.machine()}"))
+
+
+def cpu_sampler_baseline(torch, np, sets, requests=16):
+    """Reference sampling stage on the CPU: fp32 softmax of the rows, one
+    multinomial per request, ancestral walk."""
+    from oracle import oracle
+    threads = oracle.cpu_threads()
+    torch.set_num_threads(threads)
+    st = sets[0]
+    wl = st["wl"]
+    rows = int(wl.row_offset[requests])
+    logits = st["logits"][:rows].cpu()
+    t0 = time.perf_counter()
+    oracle.reference_sampling_wave(logits, wl.row_offset[:requests + 1],
+                                   wl.parents[:requests], wl.tokens[:requests],
+                                   list(range(requests)))
+    elapsed = time.perf_counter() - t0
+    return dict(value=rows / elapsed, unit="nodes/s", cores=threads, kind="port",
+                sample=f"{requests} of 64 requests ({rows} nodes, vocab {wl.vocab}): fp32 "
+                       f"softmax + multinomial + walk, {elapsed:.2f} s")
+
+
+def read_traffic():
+    path = ROOT / "profiles" / "tree_attn_qwen3_8b_traffic.json"
+    if not path.exists():
+        return None
+    try:
+        return json.loads(path.read_text()).get("hbm_bytes_per_launch")
+    except (ValueError, OSError):
+        return None
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(the path shards by request with no collective; see the sharding "
+              "design notes)", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    from specgrove_amd import ops
+    from specgrove_amd import workloads as W
+
+    device = torch.device("cuda:0")
+    torch.cuda.init()
+    steps, warmup = args.steps, args.warmup
+    wl, plan, meta, sets = build_attention_sets(torch, np, W, ops, device,
+                                                3 * (steps + warmup) + 16)
+    rows = wl.total_rows
+
+    def step(k):
+        st = sets[k % N_SETS]
+        attention_call(ops, wl, plan, meta, st)
+        commit_call(ops, wl, meta, st)
+
+    for k in range(warmup):
+        step(k)
+    torch.cuda.synchronize()
+    start, end = _events(torch, 2)
+    start.record()
+    for k in range(steps):
+        step(k)
+    end.record()
+    torch.cuda.synchronize()
+    ms_per_step = start.elapsed_time(end) / steps
+
+    attn_ms = time_calls(torch, lambda k: attention_call(ops, wl, plan, meta, sets[k % N_SETS]),
+                         steps)
+    commit_ms = time_calls(torch, lambda k: commit_call(ops, wl, meta, sets[k % N_SETS]), steps)
+    attn_avg = statistics.fmean(attn_ms)
+    attn_med = statistics.median(attn_ms)
+    attn_bytes = wl.algorithmic_bytes()
+    attn_flops = wl.algorithmic_flops()
+    achieved = attn_bytes / (attn_avg * 1e-3) / 1e9
+    commit_avg = statistics.fmean(commit_ms)
+
+    result = {
+        "metric": "packed-verify rows/s at Qwen3-8B shape",
+        "value": rows / (ms_per_step * 1e-3),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "qwen3_8b packed verify: 1 attention layer (32q/8kv, D128) + KV "
+                        "commit; 64 requests, 2048 rows, prefixes U{512..4096}",
+            "requests": wl.num_requests,
+            "packed_rows": rows,
+            "prefix_tokens": int(wl.prefix_len.sum()),
+            "tiers": {str(k): int(v) for k, v in zip(*np.unique(wl.rows, return_counts=True))},
+            "input_sets": N_SETS,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": read_traffic(),
+            "kernel": "sg_tree_attn_fwd (tree_attn_kernel<128> + merge)",
+            "algorithmic_bytes": attn_bytes,
+        },
+        "attention": {
+            "us_avg": attn_avg * 1e3,
+            "us_median": attn_med * 1e3,
+            "rows_per_s": rows / (attn_avg * 1e-3),
+            "gbs": achieved,
+            "tflops": attn_flops / (attn_avg * 1e-3) / 1e12,
+            "mfma_frac": attn_flops / (attn_avg * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+            "plan_units": plan.units,
+            "plan_merges": plan.merges,
+        },
+        "commit": {
+            "us_avg": commit_avg * 1e3,
+            "rows": int(sum(len(k) for k in wl.keep)),
+            "gbs": wl.commit_bytes() / (commit_avg * 1e-3) / 1e9,
+        },
+    }
+
+    samp_sets = None
+    if not args.no_sampler:
+        swl, samp_ms, samp_sets = sampler_bench(torch, W, ops, device, steps, warmup)
+        savg = statistics.fmean(samp_ms)
+        sbytes = swl.algorithmic_bytes()
+        result["sampler"] = {
+            "workload": swl.name,
+            "us_avg": savg * 1e3,
+            "us_median": statistics.median(samp_ms) * 1e3,
+            "nodes_per_s": swl.total_rows / (savg * 1e-3),
+            "gbs": sbytes / (savg * 1e-3) / 1e9,
+            "frac": sbytes / (savg * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "algorithmic_bytes": sbytes,
+        }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_attention_baseline(torch, np, W, args.cpu_requests)
+        if samp_sets is not None:
+            result["cpu_baseline_sampler"] = cpu_sampler_baseline(torch, np, samp_sets)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -355,3 +355,22 @@ def cpu_threads() -> int:
         return len(os.sched_getaffinity(0))
     except AttributeError:
         return os.cpu_count() or 1
+
+
+# --------------------------------------------------------------------------
+# Reference CPU path of the sampling stage (CPU baseline)
+# --------------------------------------------------------------------------
+
+def reference_sampling_wave(logits, row_offset, parents_list, tokens_list, seeds):
+    """fp32 softmax over the whole wave (sampling.py:29-36 via CTBD:1821-1824),
+    then per request one multinomial over its rows and the ancestral walk
+    (sampling.py:903-950).  Returns [(nodes, tokens, bonus)] per request."""
+    import torch
+    probs = torch.softmax(torch.as_tensor(logits).to(torch.float32), dim=-1)
+    results = []
+    for i, (parents, tokens) in enumerate(zip(parents_list, tokens_list)):
+        r0, r1 = int(row_offset[i]), int(row_offset[i + 1])
+        gen = torch.Generator().manual_seed(int(seeds[i]))
+        draws = torch.multinomial(probs[r0:r1], 1, generator=gen).reshape(-1).tolist()
+        results.append(ancestral_walk(parents, tokens, draws))
+    return results

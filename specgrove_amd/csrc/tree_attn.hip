@@ -8,24 +8,32 @@
 // reference's dense packed mask (continuous_tree_block_decode.py:500-546 and
 // tree.py:19-26) evaluated without materialising the mask or copying prefixes.
 //
-// Decomposition (MI355X): a work unit is (request, kv head, tile of up to
-// 128/G query rows = 128 query vectors, range of prefix keys); the last unit
-// of a request's key range also covers the tree rows.  A workgroup is four
-// wavefronts; wavefront w owns 32 query vectors.  Per 64-key tile:
-//   S^T[key, q] = K Q^T  with v_mfma_f32_32x32x16_bf16 (A = K rows from LDS,
-//                        B = Q from registers),
-//   online softmax per query column (one lane pair per query),
-//   O^T[d, q] += V^T P^T with the same MFMA (A = V^T rows from LDS, B = P in
-//                        registers).
-// K rows are written to LDS in the permuted order pi (LDS row i of a 32-key
-// block holds key pi(i) = 16*((i>>2)&1) + 4*(i>>3) + (i&3)) so that the MFMA
-// result gives each lane 16 consecutive keys; V is stored transposed with the
-// same permutation on head-dim rows so the output gives each lane 16
-// consecutive head dims.  Tiles are double-buffered in LDS; rows of an unfinished
-// key range are combined by a split-K merge kernel in log2 space.
+// Decomposition (MI355X, one 8-wave workgroup per CU):
+//   unit      = (request, kv head, tile of up to 128/G query rows = 128 query
+//               vectors = four 32-vector q-groups, range of prefix keys); the
+//               unit that ends a request's key range also covers its tree rows;
+//   iteration = one 128-key tile of K and V moved HBM -> LDS by
+//               global_load_lds_dwordx4 (no register staging), double-buffered,
+//               split into four 32-key blocks;
+//   wave      = one q-group x a subset of the tile's key blocks: with 3-4
+//               q-groups two waves share a q-group (two blocks each), with 1-2
+//               q-groups four waves share it (one block each).  Every wave runs
+//               its own online softmax; the waves of a q-group are merged
+//               through LDS at the end, so the serial chain of a unit is a
+//               quarter or half of its keys per wave.
+// Per 32-key block a wave computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16
+// (A = K rows from LDS stored in the permuted order pi, so the result gives
+// each lane 16 consecutive keys; B = Q in registers) and O^T += V^T P^T with
+// the same MFMA (A = V read transposed from row-major LDS by ds_read_b64_tr_b16,
+// B = P in registers).  LDS rows are unpadded; the 16-byte chunk c of row r is
+// stored at chunk c ^ swz(r) so that both read patterns are bank-conflict free.
+// Split key ranges (only when a wave has fewer units than CUs) leave
+// unnormalised partials that a second kernel combines.
 #include <algorithm>
+#include <climits>
 #include <cstring>
 #include <numeric>
+#include <type_traits>
 #include <vector>
 
 #include "sg_common.h"
@@ -35,14 +43,21 @@ namespace {
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(16))) float floatx16;
+typedef __attribute__((ext_vector_type(4))) short short4_t;
+typedef __attribute__((ext_vector_type(8))) short short8_t;
+typedef __attribute__((address_space(3))) short4_t lds_short4;
 
-constexpr int kAttnThreads = 256;
+constexpr int kThreads = 512;
 constexpr int kQPerUnit = 128;
-constexpr int kKeyTile = 64;
+constexpr int kTileKeys = 64;
+constexpr int kStages = 4;
+constexpr int kWaves = 8;
 constexpr int kMaxTreeRows = 256;
 constexpr int kAncWords = kMaxTreeRows / 32;
+constexpr int kMergeThreads = 256;
 constexpr int32_t kPlanMagic = 0x53475041;  // "SGPA"
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kDefaultCUs = 256;
 
 struct PlanHeader {
   int32_t magic;
@@ -63,9 +78,14 @@ struct AttnUnit {
   int32_t row_count;
   int32_t key_begin;
   int32_t key_end;
-  int32_t partial;  // -1: write the final output
-  int32_t flags;    // bit 0: attend to the request's tree rows
+  int32_t partial;        // partial slot of this unit, -1 when unsplit
+  int32_t flags;          // bit 0: attend to the request's tree rows
+  int32_t group;          // split group (merge record index), -1 when unsplit
+  int32_t num_splits;     // units in the group
+  int32_t first_partial;  // partial slot of the group's first unit
+  int32_t pad;
 };
+static_assert(sizeof(AttnUnit) == 48, "unit record is 48 bytes");
 
 struct MergeGroup {
   int32_t req;
@@ -87,26 +107,96 @@ __device__ __forceinline__ int key_slot(int k) {
   return 8 * ((k >> 2) & 3) + 4 * (k >> 4) + (k & 3);
 }
 
+// Key held by LDS row i of a 32-key K block (pi).
+__device__ __forceinline__ int key_pi(int i) {
+  return 16 * ((i >> 2) & 1) + 4 * (i >> 3) + (i & 3);
+}
+
+// XOR swizzles of the 16-byte chunks of LDS row r, chosen by exhaustive check
+// of every read pattern of this kernel against both 32- and 64-bank LDS:
+//   K rows (ds_read_b128, 16 consecutive rows at one chunk): r & 15 (D=128),
+//     r & 7 (D=64, 8 chunks per row);
+//   V rows (ds_read_b64_tr_b16, 4 consecutive rows at 2-4 adjacent chunks):
+//     4*(r&3) + 2*((r>>1)&1) (D=128), 2*(r&3) (D=64).
+template <int D>
+__host__ __device__ constexpr int swz_k(int r) {
+  return D == 128 ? (r & 15) : (r & 7);
+}
+template <int D>
+__host__ __device__ constexpr int swz_v(int r) {
+  return D == 128 ? 4 * (r & 3) + 2 * ((r >> 1) & 1) : 2 * (r & 3);
+}
+
+// 16-byte HBM -> LDS DMA of every lane: lane i's bytes at gbase + voff land at
+// LDS byte lds + 16*i.  Issued as inline assembly so that the compiler does not
+// model it: its automatic waits would otherwise stall the first LDS read of the
+// other pipeline stage on this in-flight copy.  The kernel waits for the DMAs
+// explicitly (s_waitcnt vmcnt(0)) before the barrier that publishes the tile.
+// m0 is written here; nothing else in the kernel reads m0.
+__device__ __forceinline__ void dma16(const void* gbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(lds), "v"(voff), "s"(gbase)
+               : "memory");
+}
+
+// s_waitcnt immediate that waits for vmcnt <= n and leaves the other counters
+// unconstrained (gfx9 layout: vmcnt bits [3:0] and [15:14], expcnt [6:4],
+// lgkmcnt [11:8]).
+constexpr int vmcnt_encoding(int n) {
+  return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8);
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p));
+}
+
+// max / sum of a value with the same lane of the other 32-lane half.
+__device__ __forceinline__ float half_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                  false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                  false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 __device__ __forceinline__ uint4 zero4() { return make_uint4(0u, 0u, 0u, 0u); }
 
+enum class Mask { kFull, kLimit, kTree };
+template <Mask M>
+using MaskTag = std::integral_constant<Mask, M>;
+template <int N>
+using IntTag = std::integral_constant<int, N>;
+
+// Per-wave attention state: one query column per lane pair.
 template <int D>
-struct TileRegs {
-  uint4 k[D / 32];  // 64 keys * D/8 chunks / 256 threads
-  uint4 v[4];       // 4 consecutive keys of one 8-wide head-dim chunk
+struct WaveState {
+  float m;  // running max of raw scores
+  float l;  // running sum of exp2((s - m) * c2)
+  floatx16 acc[D / 32];
 };
 
 template <int D>
-__global__ __launch_bounds__(kAttnThreads, 2) void tree_attn_kernel(SgTreeAttnArgs a) {
-  constexpr int KB = D / 16;       // QK^T k-blocks
-  constexpr int DB = D / 32;       // PV d-blocks
-  constexpr int DC = D / 8;        // 16-byte chunks per row
-  constexpr int KS = D + 8;        // K row stride in LDS (bf16)
-  constexpr int VS = kKeyTile + 8; // V^T row stride in LDS (bf16)
-  constexpr int KLOADS = D / 32;
-  __shared__ __align__(16) uint16_t s_k[2][kKeyTile * KS];
-  __shared__ __align__(16) uint16_t s_v[2][D * VS];
+__global__ __launch_bounds__(kThreads, 1) void tree_attn_kernel(SgTreeAttnArgs a) {
+  constexpr int KB = D / 16;                     // QK^T k-blocks of 16 head dims
+  constexpr int DB = D / 32;                     // PV blocks of 32 head dims
+  constexpr int ROWB = D * 2;                    // bytes per unpadded K/V row
+  constexpr int STAGEB = kTileKeys * ROWB;       // bytes of one K (or V) tile
+  constexpr int ROWS_PER_KB = 1024 / ROWB;       // rows covered by one wave DMA
+  constexpr int DMAS = STAGEB / 1024 / kWaves;   // DMAs per wave per K (or V) tile
+  constexpr int STATE = 2 + 16 * DB;             // floats per lane of a WaveState
+  static_assert(DMAS >= 1, "tile too small for the workgroup");
+  static_assert(kStages * STAGEB <= 65536, "ring offsets must fit the LDS immediate");
+  static_assert(2 * kStages * STAGEB >= 6 * STATE * 64 * 4, "merge scratch");
+  // Ring of kStages tiles of K and of V; reused as the merge scratch at the end.
+  __shared__ __align__(1024) unsigned char s_k[kStages * STAGEB];
+  __shared__ __align__(1024) unsigned char s_v[kStages * STAGEB];
   __shared__ uint32_t s_anc[kQPerUnit][kAncWords];
   __shared__ int s_parent[kMaxTreeRows];
 
@@ -115,23 +205,36 @@ __global__ __launch_bounds__(kAttnThreads, 2) void tree_attn_kernel(SgTreeAttnAr
   const int G = a.num_q_heads / a.num_kv_heads;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5;
   const int col = lane & 31;
-  const int m = wave * 32 + col;        // query vector inside the unit
-  const int r_local = m / G;            // query row inside the tile
+  const int nq = (u.row_count * G + 31) / 32;   // q-groups in use, 1..4
+  // Waves sharing a q-group: 4 when the unit has 1-2 q-groups (they take the
+  // four 32-key blocks of two consecutive tiles), else 2 (the two blocks of one
+  // tile).  Either way every wave handles one 32-key block per iteration.
+  const int streams = nq <= 2 ? 4 : 2;
+  const int per_iter = streams / 2;             // tiles consumed per iteration
+  const int qg = wave % nq;
+  const int ks = wave / nq;                     // key stream of this wave
+  const bool active = ks < streams;
+  const int my_tile = ks >> 1;                  // tile of the iteration this wave takes
+  const int my_blk = ks & 1;                    // 32-key block inside that tile
+  const int m = qg * 32 + col;                  // query vector inside the unit
+  const int r_local = m / G;                    // query row inside the tile
   const int head = u.kv_head * G + (m - r_local * G);
-  const bool q_valid = r_local < u.row_count;
+  const bool q_valid = active && r_local < u.row_count;
   const int r0 = a.row_offset_dev[u.req];
-  const int n = a.row_offset_dev[u.req + 1] - r0;
+  // The planner bounds tree sizes; clamping keeps a mismatched device row_offset
+  // inside the LDS tables.
+  const int n = min(a.row_offset_dev[u.req + 1] - r0, kMaxTreeRows);
   const int64_t row = static_cast<int64_t>(r0) + u.row_begin + r_local;
   const int g = u.kv_head;
   const bool do_tree = (u.flags & 1) != 0;
 
   // Ancestor-or-self bitsets of the tile's rows (request-local numbering).
   if (do_tree) {
-    for (int k = tid; k < n; k += kAttnThreads) s_parent[k] = a.parent_dev[r0 + k];
-    for (int k = tid; k < kQPerUnit * kAncWords; k += kAttnThreads) (&s_anc[0][0])[k] = 0u;
+    for (int k = tid; k < n; k += kThreads) s_parent[k] = a.parent_dev[r0 + k];
+    for (int k = tid; k < kQPerUnit * kAncWords; k += kThreads) (&s_anc[0][0])[k] = 0u;
     __syncthreads();
     if (tid < u.row_count) {
       int node = u.row_begin + tid;
@@ -139,7 +242,9 @@ __global__ __launch_bounds__(kAttnThreads, 2) void tree_attn_kernel(SgTreeAttnAr
 #pragma unroll
       for (int w = 0; w < kAncWords; ++w) bits[w] = 0u;
       for (int guard = 0; node >= 0 && guard < kMaxTreeRows; ++guard) {
-        bits[node >> 5] |= 1u << (node & 31);
+#pragma unroll
+        for (int w = 0; w < kAncWords; ++w)
+          bits[w] |= (w == (node >> 5)) ? (1u << (node & 31)) : 0u;
         const int p = s_parent[node];
         node = (p < node) ? p : -1;
       }
@@ -159,240 +264,352 @@ __global__ __launch_bounds__(kAttnThreads, 2) void tree_attn_kernel(SgTreeAttnAr
   }
 
   const int prefix_keys = u.key_end - u.key_begin;
-  const int tiles_prefix = (prefix_keys + kKeyTile - 1) / kKeyTile;
-  const int tiles_tree = do_tree ? (n + kKeyTile - 1) / kKeyTile : 0;
+  const int tiles_prefix = (prefix_keys + kTileKeys - 1) / kTileKeys;
+  const int tiles_full = prefix_keys / kTileKeys;
+  const int tiles_tree = do_tree ? (n + kTileKeys - 1) / kTileKeys : 0;
   const int tiles = tiles_prefix + tiles_tree;
-  const int64_t prefix_token0 = a.prefix_start_dev[u.req] + u.key_begin;
-  const uint16_t* kc = static_cast<const uint16_t*>(a.k_cache_dev) + g * a.cache_head_stride;
-  const uint16_t* vc = static_cast<const uint16_t*>(a.v_cache_dev) + g * a.cache_head_stride;
-  const uint16_t* kt = static_cast<const uint16_t*>(a.k_tree_dev) + g * a.tree_head_stride;
-  const uint16_t* vt = static_cast<const uint16_t*>(a.v_tree_dev) + g * a.tree_head_stride;
+  const int64_t prefix0 = a.prefix_start_dev[u.req] + u.key_begin;
+  const uint16_t* kc = static_cast<const uint16_t*>(a.k_cache_dev) + g * a.cache_head_stride +
+                       prefix0 * a.cache_token_stride;
+  const uint16_t* vc = static_cast<const uint16_t*>(a.v_cache_dev) + g * a.cache_head_stride +
+                       prefix0 * a.cache_token_stride;
+  const uint16_t* kt = static_cast<const uint16_t*>(a.k_tree_dev) + g * a.tree_head_stride +
+                       static_cast<int64_t>(r0) * a.tree_row_stride;
+  const uint16_t* vt = static_cast<const uint16_t*>(a.v_tree_dev) + g * a.tree_head_stride +
+                       static_cast<int64_t>(r0) * a.tree_row_stride;
 
-  auto key_address = [&](bool tree, int key, const uint16_t* cache, const uint16_t* tree_base,
-                         int t) -> const uint16_t* {
-    if (!tree) return cache + (prefix_token0 + static_cast<int64_t>(t) * kKeyTile + key) * a.cache_token_stride;
-    return tree_base + (static_cast<int64_t>(r0) + (t - tiles_prefix) * kKeyTile + key) * a.tree_row_stride;
-  };
-
-  TileRegs<D> regs;
+  // DMA slots of this lane: wave DMA i of a tile covers LDS rows
+  // ROWS_PER_KB*(wave*DMAS + i) + lane / (ROWB/16), physical chunk lane % (ROWB/16);
+  // the row holds key pi(row) for K and key row for V.  Full prefix tiles use
+  // precomputed lane offsets; the last partial tile and tree tiles clamp the key.
+  const int cstride = static_cast<int>(a.cache_token_stride);
+  uint32_t k_dma[DMAS], v_dma[DMAS];
+#pragma unroll
+  for (int i = 0; i < DMAS; ++i) {
+    const int lds_row = ROWS_PER_KB * (wave * DMAS + i) + lane / (ROWB / 16);
+    const int phys = lane % (ROWB / 16);
+    const int kk = (lds_row & ~31) + key_pi(lds_row & 31);
+    k_dma[i] = static_cast<uint32_t>(2 * (kk * cstride + 8 * (phys ^ swz_k<D>(lds_row))));
+    v_dma[i] = static_cast<uint32_t>(2 * (lds_row * cstride + 8 * (phys ^ swz_v<D>(lds_row))));
+  }
   auto load_tile = [&](int t) {
+    if (t >= tiles) return;
+    const int stage = t % kStages;
+    const uint32_t kdst = lds_addr(s_k + stage * STAGEB + wave * DMAS * 1024);
+    const uint32_t vdst = lds_addr(s_v + stage * STAGEB + wave * DMAS * 1024);
+    if (t < tiles_full) {
+      const unsigned char* kb0 =
+          reinterpret_cast<const unsigned char*>(kc + static_cast<int64_t>(t) * kTileKeys * cstride);
+      const unsigned char* vb0 =
+          reinterpret_cast<const unsigned char*>(vc + static_cast<int64_t>(t) * kTileKeys * cstride);
+#pragma unroll
+      for (int i = 0; i < DMAS; ++i) {
+        dma16(kb0, k_dma[i], kdst + 1024 * i);
+        dma16(vb0, v_dma[i], vdst + 1024 * i);
+      }
+      return;
+    }
     const bool tree = t >= tiles_prefix;
-    const int limit = tree ? n - (t - tiles_prefix) * kKeyTile : prefix_keys - t * kKeyTile;
+    const int key0 = tree ? (t - tiles_prefix) * kTileKeys : t * kTileKeys;
+    const int last = (tree ? n : prefix_keys) - key0 - 1;
+    const int stride = tree ? static_cast<int>(a.tree_row_stride) : cstride;
+    const unsigned char* kb0 = reinterpret_cast<const unsigned char*>(
+        (tree ? kt : kc) + static_cast<int64_t>(key0) * stride);
+    const unsigned char* vb0 = reinterpret_cast<const unsigned char*>(
+        (tree ? vt : vc) + static_cast<int64_t>(key0) * stride);
 #pragma unroll
-    for (int i = 0; i < KLOADS; ++i) {
-      const int c = tid + kAttnThreads * i;
-      const int key = c / DC;
-      const int dc = c - key * DC;
-      regs.k[i] = key < limit
-                      ? *reinterpret_cast<const uint4*>(key_address(tree, key, kc, kt, t) + 8 * dc)
-                      : zero4();
-    }
-    if (tid < 16 * DC) {
-      const int kg = tid / DC;
-      const int dc = tid - kg * DC;
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const int key = 4 * kg + kk;
-        regs.v[kk] = key < limit
-                         ? *reinterpret_cast<const uint4*>(key_address(tree, key, vc, vt, t) + 8 * dc)
-                         : zero4();
-      }
-    }
-  };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < KLOADS; ++i) {
-      const int c = tid + kAttnThreads * i;
-      const int key = c / DC;
-      const int dc = c - key * DC;
-      const int slot = (key & ~31) + key_slot(key & 31);
-      *reinterpret_cast<uint4*>(&s_k[buf][slot * KS + 8 * dc]) = regs.k[i];
-    }
-    if (tid < 16 * DC) {
-      const int kg = tid / DC;
-      const int dc = tid - kg * DC;
-      const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&regs.v[0]);
-      const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&regs.v[1]);
-      const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&regs.v[2]);
-      const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&regs.v[3]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int sh = (e & 1) * 16;
-        const uint32_t x0 = (w0[e >> 1] >> sh) & 0xffffu;
-        const uint32_t x1 = (w1[e >> 1] >> sh) & 0xffffu;
-        const uint32_t x2 = (w2[e >> 1] >> sh) & 0xffffu;
-        const uint32_t x3 = (w3[e >> 1] >> sh) & 0xffffu;
-        const int d = 8 * dc + e;
-        const int vrow = (d & ~31) + key_slot(d & 31);
-        uint2 packed;
-        packed.x = x0 | (x1 << 16);
-        packed.y = x2 | (x3 << 16);
-        *reinterpret_cast<uint2*>(&s_v[buf][vrow * VS + 4 * kg]) = packed;
-      }
+    for (int i = 0; i < DMAS; ++i) {
+      const int lds_row = ROWS_PER_KB * (wave * DMAS + i) + lane / (ROWB / 16);
+      const int phys = lane % (ROWB / 16);
+      // Keys past the range re-read the last valid key: finite data that the
+      // score mask (K) or a zero probability (V) removes.
+      const int kk = min((lds_row & ~31) + key_pi(lds_row & 31), last);
+      const int vk = min(lds_row, last);
+      dma16(kb0, static_cast<uint32_t>(2 * (kk * stride + 8 * (phys ^ swz_k<D>(lds_row)))),
+            kdst + 1024 * i);
+      dma16(vb0, static_cast<uint32_t>(2 * (vk * stride + 8 * (phys ^ swz_v<D>(lds_row)))),
+            vdst + 1024 * i);
     }
   };
 
-  const float sl2 = a.scale * kLog2e;
-  float m_run = -__builtin_inff();
-  float l_run = 0.0f;
-  floatx16 acc[DB];
+  // Lane parts of the LDS read addresses (bytes), including this wave's tile
+  // offset inside the iteration and its block inside the tile; the ring stage
+  // is a compile-time immediate.
+  const int gq = lane >> 4;
+  const int jj = lane & 15;
+  const int rr = jj >> 2;
+  const int cc = jj & 3;
+  int k_off[KB];
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb)
+    k_off[kb] = my_tile * STAGEB + (32 * my_blk + col) * ROWB +
+                16 * ((2 * kb + half) ^ swz_k<D>(col));
+  int v_off[DB][2];
 #pragma unroll
   for (int db = 0; db < DB; ++db)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[db][r] = 0.0f;
+    for (int hi = 0; hi < 2; ++hi) {
+      const int vrow = 16 * half + 4 * hi + rr;
+      const int chunk = 4 * db + 2 * (gq & 1) + (cc >> 1);
+      v_off[db][hi] = my_tile * STAGEB + (32 * my_blk + vrow) * ROWB +
+                      16 * (chunk ^ swz_v<D>(vrow)) + 8 * (cc & 1);
+    }
 
-  if (tiles > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
-  __syncthreads();
-  for (int t = 0; t < tiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < tiles) load_tile(t + 1);
-    const bool tree = t >= tiles_prefix;
-    const int key0 = tree ? (t - tiles_prefix) * kKeyTile : t * kKeyTile;
-    const int limit = tree ? n : prefix_keys;
-
-    float x[2][16];
+  const float c2 = a.scale * kLog2e;
+  WaveState<D> st;
+  st.m = -__builtin_inff();
+  st.l = 0.0f;
 #pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) st.acc[db][r] = 0.0f;
+
+  // This wave's 32-key block of ring stage S: S^T, online softmax, O^T.
+  // key0 = first key of the block's tile (for masks), limit = keys in range.
+  auto compute = [&](auto stage_tag, auto mode_tag, int key0, int limit) {
+    constexpr int kStage = decltype(stage_tag)::value;
+    constexpr Mask kMode = decltype(mode_tag)::value;
+    const unsigned char* sk = s_k + kStage * STAGEB;
+    const unsigned char* sv = s_v + kStage * STAGEB;
+    float x[16];
+    {
       floatx16 s;
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[r] = 0.0f;
-      const uint16_t* krow = &s_k[buf][(32 * blk + col) * KS + 8 * half];
+      bf16x8 kf[KB];
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        const bf16x8 kf = as_bf16x8(*reinterpret_cast<const uint4*>(krow + 16 * kb));
-        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kb], s, 0, 0, 0);
-      }
+      for (int kb = 0; kb < KB; ++kb)
+        kf[kb] = as_bf16x8(*reinterpret_cast<const uint4*>(sk + k_off[kb]));
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kb], qf[kb], s, 0, 0, 0);
+      const int first = key0 + 32 * my_blk + 16 * half;
+      uint32_t bits = 0xffffffffu;
+      if (kMode == Mask::kTree) bits = s_anc[r_local][(key0 + 32 * my_blk) >> 5] >> (16 * half);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int key = key0 + 32 * blk + 16 * half + r;
-        bool visible = key < limit;
-        if (tree && visible) visible = (s_anc[r_local < kQPerUnit ? r_local : 0][key >> 5] >> (key & 31)) & 1u;
-        x[blk][r] = visible ? s[r] * sl2 : -__builtin_inff();
+        bool visible = true;
+        if (kMode != Mask::kFull) visible = first + r < limit;
+        if (kMode == Mask::kTree) visible = visible && ((bits >> r) & 1u);
+        x[r] = visible ? s[r] : -__builtin_inff();
       }
     }
-    float tmax = x[0][0];
+    float tmax = x[0];
 #pragma unroll
-    for (int blk = 0; blk < 2; ++blk)
+    for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, x[r]);
+    tmax = half_max(tmax);
+    const float m_new = fmaxf(st.m, tmax);
+    if (__ballot(m_new > st.m)) {
+      const float alpha = (st.m == -__builtin_inff()) ? 0.0f
+                                                       : __builtin_amdgcn_exp2f((st.m - m_new) * c2);
+      st.l *= alpha;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, x[blk][r]);
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const float m_new = fmaxf(m_run, tmax);
-    const float m_use = (m_new == -__builtin_inff()) ? 0.0f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) st.acc[db][r] *= alpha;
+      st.m = m_new;
+    }
+    const float mc = (st.m == -__builtin_inff()) ? 0.0f : st.m * c2;
     float psum = 0.0f;
 #pragma unroll
-    for (int blk = 0; blk < 2; ++blk)
+    for (int r = 0; r < 16; ++r) {
+      x[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[r], c2, -mc));
+      psum += x[r];
+    }
+    st.l += half_sum(psum);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        x[blk][r] = __builtin_amdgcn_exp2f(x[blk][r] - m_use);
-        psum += x[blk][r];
+    for (int c = 0; c < 2; ++c) {
+      bf16x8 pf;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pf[e] = static_cast<__bf16>(x[8 * c + e]);
+      const unsigned char* vrows = sv + 8 * c * ROWB;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const short4_t lo =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(vrows + v_off[db][0]));
+        const short4_t hi =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(vrows + v_off[db][1]));
+        const short8_t both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        st.acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, both),
+                                                             pf, st.acc[db], 0, 0, 0);
       }
-    psum += __shfl_xor(psum, 32);
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
+    }
+  };
+
+  // Pipeline: tiles t0 .. t0+per_iter-1 are computed while the next
+  // kStages-per_iter tiles stream in.  Each tile is DMAS K + DMAS V
+  // instructions per wave, so "everything but the newest j tiles has landed"
+  // is vmcnt(2*DMAS*j).
+  const int ahead = kStages - per_iter;
+  auto wait_tiles = [&](int newer) {
+    if (newer >= 2) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_encoding(4 * DMAS));
+    } else if (newer == 1) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_encoding(2 * DMAS));
+    } else {
+      __builtin_amdgcn_s_waitcnt(0);
+    }
+  };
+  for (int t = 0; t < ahead; ++t) load_tile(t);
+
+  // Iteration over tile groups t0 = per_iter*i.  The wave's tile is
+  // t0 + my_tile, in ring stage (t0 % kStages) + my_tile (no wrap: per_iter
+  // divides kStages and t0 is a multiple of per_iter).
+  auto iterate = [&](int t0, auto base_tag) {
+    constexpr int kBase = decltype(base_tag)::value;
+    const int issued = min(tiles, t0 + ahead);
+    wait_tiles(issued - min(tiles, t0 + per_iter));
+    __syncthreads();
+    for (int k = 0; k < per_iter; ++k) load_tile(t0 + ahead + k);
+    const int t = t0 + my_tile;
+    if (!active || t >= tiles) return;
+    if (t < tiles_full) {
+      compute(IntTag<kBase>{}, MaskTag<Mask::kFull>{}, 0, 0);
+    } else if (t < tiles_prefix) {
+      compute(IntTag<kBase>{}, MaskTag<Mask::kLimit>{}, t * kTileKeys, prefix_keys);
+    } else {
+      compute(IntTag<kBase>{}, MaskTag<Mask::kTree>{}, (t - tiles_prefix) * kTileKeys, n);
+    }
+  };
+  int t0 = 0;
+  if (per_iter == 1) {
+    for (; t0 + 4 <= tiles; t0 += 4) {
+      iterate(t0, IntTag<0>{});
+      iterate(t0 + 1, IntTag<1>{});
+      iterate(t0 + 2, IntTag<2>{});
+      iterate(t0 + 3, IntTag<3>{});
+    }
+    if (t0 < tiles) iterate(t0++, IntTag<0>{});
+    if (t0 < tiles) iterate(t0++, IntTag<1>{});
+    if (t0 < tiles) iterate(t0++, IntTag<2>{});
+  } else {
+    for (; t0 + 4 <= tiles; t0 += 4) {
+      iterate(t0, IntTag<0>{});
+      iterate(t0 + 2, IntTag<2>{});
+    }
+    if (t0 < tiles) iterate(t0, IntTag<0>{});
+    if (t0 + 2 < tiles) iterate(t0 + 2, IntTag<2>{});
+  }
+  __syncthreads();
+
+  // Merge the key streams of each q-group through LDS (the ring is free now).
+  // Slot k (k = (ks-1)*nq + qg < 6) lives at float offset k*STATE*64 of s_k|s_v.
+  auto merge_slot = [&](int k) -> float* {
+    constexpr int kPerBuf = (kStages * STAGEB) / (STATE * 64 * 4);
+    unsigned char* buf = (k < kPerBuf) ? s_k : s_v;
+    return reinterpret_cast<float*>(buf) + static_cast<size_t>(k % kPerBuf) * STATE * 64;
+  };
+  if (active && ks > 0) {
+    float* slot = merge_slot((ks - 1) * nq + qg);
+    slot[lane] = st.m;
+    slot[64 + lane] = st.l;
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
-
+      for (int r = 0; r < 16; ++r) slot[(2 + 16 * db + r) * 64 + lane] = st.acc[db][r];
+  }
+  __syncthreads();
+  if (!active || ks > 0) return;
+  {
+    float m_all = st.m;
+    for (int s = 1; s < streams; ++s) m_all = fmaxf(m_all, merge_slot((s - 1) * nq + qg)[lane]);
+    const float m_use = (m_all == -__builtin_inff()) ? 0.0f : m_all;
+    const float w0 = (st.m == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f((st.m - m_use) * c2);
+    st.l *= w0;
 #pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
+    for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        bf16x8 pf;
+      for (int r = 0; r < 16; ++r) st.acc[db][r] *= w0;
+    for (int s = 1; s < streams; ++s) {
+      const float* slot = merge_slot((s - 1) * nq + qg);
+      const float ms = slot[lane];
+      const float w = (ms == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f((ms - m_use) * c2);
+      st.l += w * slot[64 + lane];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) pf[e] = static_cast<__bf16>(x[blk][8 * c + e]);
+      for (int db = 0; db < DB; ++db)
 #pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          const uint16_t* vrow = &s_v[buf][(32 * db + col) * VS + 32 * blk + 16 * half + 8 * c];
-          const bf16x8 vf = as_bf16x8(*reinterpret_cast<const uint4*>(vrow));
-          acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, acc[db], 0, 0, 0);
-        }
-      }
+        for (int r = 0; r < 16; ++r) st.acc[db][r] += w * slot[(2 + 16 * db + r) * 64 + lane];
     }
-    if (t + 1 < tiles) store_tile(buf ^ 1);
-    __syncthreads();
+    st.m = m_all;
   }
 
-  if (!q_valid) return;
-  if (u.partial < 0) {
-    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-    uint16_t* op = static_cast<uint16_t*>(a.out_dev) + row * a.out_row_stride +
-                   static_cast<int64_t>(head) * a.out_head_stride;
-#pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      uint4 lo, hi;
-      lo.x = pack_bf16x2(acc[db][0] * inv, acc[db][1] * inv);
-      lo.y = pack_bf16x2(acc[db][2] * inv, acc[db][3] * inv);
-      lo.z = pack_bf16x2(acc[db][4] * inv, acc[db][5] * inv);
-      lo.w = pack_bf16x2(acc[db][6] * inv, acc[db][7] * inv);
-      hi.x = pack_bf16x2(acc[db][8] * inv, acc[db][9] * inv);
-      hi.y = pack_bf16x2(acc[db][10] * inv, acc[db][11] * inv);
-      hi.z = pack_bf16x2(acc[db][12] * inv, acc[db][13] * inv);
-      hi.w = pack_bf16x2(acc[db][14] * inv, acc[db][15] * inv);
-      uint16_t* dst = op + 32 * db + 16 * half;
-      *reinterpret_cast<uint4*>(dst) = lo;
-      *reinterpret_cast<uint4*>(dst + 8) = hi;
-    }
-  } else {
+  // st.acc[db][r] holds head dim 32*db + 8*(r/4) + 4*half + (r%4) of this lane's query.
+  if (u.partial >= 0) {
+    // Partial layout (floats): O as float4 chunks ((db*4 + q4)*2 + half)*128 + m,
+    // then the running max (log2 units) and sum per query vector.
     float* part = static_cast<float*>(a.workspace_dev) + partial_floats(D) * u.partial;
-    float* o = part + static_cast<size_t>(m) * D;
+    float4* o = reinterpret_cast<float4*>(part);
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      float4* dst = reinterpret_cast<float4*>(o + 32 * db + 16 * half);
+    for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int k = 0; k < 4; ++k)
-        dst[k] = make_float4(acc[db][4 * k], acc[db][4 * k + 1], acc[db][4 * k + 2],
-                             acc[db][4 * k + 3]);
-    }
+      for (int q4 = 0; q4 < 4; ++q4)
+        o[((db * 4 + q4) * 2 + half) * kQPerUnit + m] =
+            make_float4(st.acc[db][4 * q4], st.acc[db][4 * q4 + 1], st.acc[db][4 * q4 + 2],
+                        st.acc[db][4 * q4 + 3]);
     if (half == 0) {
-      part[static_cast<size_t>(kQPerUnit) * D + m] = m_run;
-      part[static_cast<size_t>(kQPerUnit) * D + kQPerUnit + m] = l_run;
+      part[static_cast<size_t>(kQPerUnit) * D + m] =
+          (st.m == -__builtin_inff()) ? st.m : st.m * c2;
+      part[static_cast<size_t>(kQPerUnit) * D + kQPerUnit + m] = st.l;
     }
+    return;
   }
+  if (!q_valid) return;
+  const float inv = st.l > 0.0f ? 1.0f / st.l : 0.0f;
+  uint16_t* op = static_cast<uint16_t*>(a.out_dev) + row * a.out_row_stride +
+                 static_cast<int64_t>(head) * a.out_head_stride + 4 * half;
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      uint2 packed;
+      packed.x = pack_bf16x2(st.acc[db][4 * q4] * inv, st.acc[db][4 * q4 + 1] * inv);
+      packed.y = pack_bf16x2(st.acc[db][4 * q4 + 2] * inv, st.acc[db][4 * q4 + 3] * inv);
+      *reinterpret_cast<uint2*>(op + 32 * db + 8 * q4) = packed;
+    }
 }
 
-// Combines the split-K partials of one (request, kv head, tile).
+// Combines the partials of one split group: thread -> (query vector, float4 chunk).
 template <int D>
-__global__ __launch_bounds__(kAttnThreads) void tree_attn_merge_kernel(SgTreeAttnArgs a) {
+__global__ __launch_bounds__(kMergeThreads) void tree_attn_merge_kernel(SgTreeAttnArgs a) {
   const PlanHeader* hdr = static_cast<const PlanHeader*>(a.plan_dev);
   const MergeGroup grp = reinterpret_cast<const MergeGroup*>(
       reinterpret_cast<const AttnUnit*>(hdr + 1) + hdr->num_units)[blockIdx.x];
   const int G = a.num_q_heads / a.num_kv_heads;
   const int r0 = a.row_offset_dev[grp.req];
   const float* ws = static_cast<const float*>(a.workspace_dev);
-  constexpr int DC4 = D / 4;
-  for (int item = threadIdx.x; item < kQPerUnit * DC4; item += kAttnThreads) {
-    const int m = item / DC4;
-    const int c = item - m * DC4;
-    const int r_local = m / G;
-    if (r_local >= grp.row_count) continue;
-    const int head = grp.kv_head * G + (m - r_local * G);
+  constexpr int CH = D / 4;  // float4 chunks per query vector
+  const int vectors = grp.row_count * G;
+  for (int item = threadIdx.x; item < CH * kQPerUnit; item += kMergeThreads) {
+    const int ch = item / kQPerUnit;  // chunk index ((db*4 + q4)*2 + half)
+    const int m = item - ch * kQPerUnit;
+    if (m >= vectors) continue;
     float mx = -__builtin_inff();
-    for (int s = 0; s < grp.num_partials; ++s) {
-      const float* part = ws + partial_floats(D) * (grp.first_partial + s);
-      mx = fmaxf(mx, part[static_cast<size_t>(kQPerUnit) * D + m]);
-    }
+    for (int s = 0; s < grp.num_partials; ++s)
+      mx = fmaxf(mx, ws[partial_floats(D) * (grp.first_partial + s) +
+                        static_cast<size_t>(kQPerUnit) * D + m]);
     const float m_use = (mx == -__builtin_inff()) ? 0.0f : mx;
     float l = 0.0f;
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int s = 0; s < grp.num_partials; ++s) {
       const float* part = ws + partial_floats(D) * (grp.first_partial + s);
-      const float w = __builtin_amdgcn_exp2f(part[static_cast<size_t>(kQPerUnit) * D + m] - m_use);
+      const float ms = part[static_cast<size_t>(kQPerUnit) * D + m];
+      const float w = (ms == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(ms - m_use);
       l += w * part[static_cast<size_t>(kQPerUnit) * D + kQPerUnit + m];
-      const float4 v = reinterpret_cast<const float4*>(part + static_cast<size_t>(m) * D)[c];
+      const float4 v = reinterpret_cast<const float4*>(part)[ch * kQPerUnit + m];
       o.x += w * v.x;
       o.y += w * v.y;
       o.z += w * v.z;
       o.w += w * v.w;
     }
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    const int r_local = m / G;
+    const int head = grp.kv_head * G + (m - r_local * G);
+    const int db = ch / 8;
+    const int q4 = (ch / 2) & 3;
+    const int hf = ch & 1;
     const int64_t row = static_cast<int64_t>(r0) + grp.row_begin + r_local;
     uint16_t* dst = static_cast<uint16_t*>(a.out_dev) + row * a.out_row_stride +
-                    static_cast<int64_t>(head) * a.out_head_stride + 4 * c;
+                    static_cast<int64_t>(head) * a.out_head_stride + 32 * db + 8 * q4 + 4 * hf;
     uint2 packed;
     packed.x = pack_bf16x2(o.x * inv, o.y * inv);
     packed.y = pack_bf16x2(o.z * inv, o.w * inv);
@@ -424,6 +641,10 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
   const int rows_per_tile = kQPerUnit / G;
   SG_REQUIRE(num_requests == 0 || row_offset_host[0] == 0, "row_offset[0] must be 0");
 
+  // Units of one (request, kv head, row tile) are split over its prefix only
+  // when the wave has too few units to give every CU work: each split costs a
+  // partial write and a merge pass.  target_units_hint overrides the target.
+  int64_t base_units = 0;
   int64_t work = 0;
   for (int i = 0; i < num_requests; ++i) {
     const int rows = row_offset_host[i + 1] - row_offset_host[i];
@@ -431,12 +652,16 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
                "every request must have between 0 and 256 packed rows");
     SG_REQUIRE(prefix_len_host[i] >= 0, "prefix lengths must be non-negative");
     const int tiles = (rows + rows_per_tile - 1) / rows_per_tile;
-    work += static_cast<int64_t>(num_kv_heads) * tiles * (prefix_len_host[i] + rows);
+    base_units += static_cast<int64_t>(num_kv_heads) * tiles;
+    work += static_cast<int64_t>(num_kv_heads) * tiles *
+            ((prefix_len_host[i] + kTileKeys - 1) / kTileKeys + 1);
   }
-  const int64_t target = target_units_hint > 0 ? target_units_hint : 1024;
-  int64_t chunk = (work + target - 1) / std::max<int64_t>(target, 1);
-  chunk = std::max<int64_t>(chunk, 512);
-  chunk = (chunk + kKeyTile - 1) / kKeyTile * kKeyTile;
+  const int64_t target = target_units_hint > 0 ? target_units_hint : kDefaultCUs;
+  int64_t chunk = INT32_MAX;
+  if (base_units > 0 && base_units < target) {
+    const int64_t per_unit = std::max<int64_t>(4, (work + target - 1) / target);
+    chunk = per_unit * kTileKeys;
+  }
 
   std::vector<AttnUnit> units;
   std::vector<MergeGroup> merges;
@@ -445,34 +670,37 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
     const int rows = row_offset_host[i + 1] - row_offset_host[i];
     if (rows == 0) continue;
     const int L = prefix_len_host[i];
-    const int splits = std::max<int64_t>(1, (L + chunk - 1) / chunk);
+    const int splits = static_cast<int>(std::max<int64_t>(1, (L + chunk / 2) / chunk));
     const int tiles = (rows + rows_per_tile - 1) / rows_per_tile;
     for (int g = 0; g < num_kv_heads; ++g) {
       for (int tile = 0; tile < tiles; ++tile) {
-        const int row_begin = tile * rows_per_tile;
-        const int row_count = std::min(rows_per_tile, rows - row_begin);
+        const int group = splits > 1 ? static_cast<int>(merges.size()) : -1;
         const int first = partials;
         for (int s = 0; s < splits; ++s) {
           AttnUnit u;
           u.req = i;
           u.kv_head = g;
-          u.row_begin = row_begin;
-          u.row_count = row_count;
-          u.key_begin = static_cast<int32_t>(static_cast<int64_t>(L) * s / splits / kKeyTile * kKeyTile);
-          u.key_end = s + 1 == splits
-                          ? L
-                          : static_cast<int32_t>(static_cast<int64_t>(L) * (s + 1) / splits /
-                                                 kKeyTile * kKeyTile);
+          u.row_begin = tile * rows_per_tile;
+          u.row_count = std::min(rows_per_tile, rows - u.row_begin);
+          u.key_begin = static_cast<int32_t>(static_cast<int64_t>(L) * s / splits / kTileKeys *
+                                             kTileKeys);
+          u.key_end = s + 1 == splits ? L
+                                      : static_cast<int32_t>(static_cast<int64_t>(L) * (s + 1) /
+                                                             splits / kTileKeys * kTileKeys);
           u.partial = splits > 1 ? partials++ : -1;
           u.flags = (s + 1 == splits) ? 1 : 0;
+          u.group = group;
+          u.num_splits = splits;
+          u.first_partial = splits > 1 ? first : -1;
+          u.pad = 0;
           units.push_back(u);
         }
         if (splits > 1) {
           MergeGroup mg;
           mg.req = i;
           mg.kv_head = g;
-          mg.row_begin = row_begin;
-          mg.row_count = row_count;
+          mg.row_begin = tile * rows_per_tile;
+          mg.row_count = std::min(rows_per_tile, rows - mg.row_begin);
           mg.first_partial = first;
           mg.num_partials = splits;
           mg.pad0 = mg.pad1 = 0;
@@ -481,19 +709,20 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
       }
     }
   }
-  // Longest units first: the dispatcher hands out workgroups in order.
+  // Longest units first: workgroups are dispatched in grid order.
   std::vector<int64_t> cost(units.size());
   for (size_t k = 0; k < units.size(); ++k) {
     const int rows = row_offset_host[units[k].req + 1] - row_offset_host[units[k].req];
-    cost[k] = (units[k].key_end - units[k].key_begin) + ((units[k].flags & 1) ? rows : 0);
+    cost[k] = (units[k].key_end - units[k].key_begin + kTileKeys - 1) / kTileKeys +
+              ((units[k].flags & 1) ? (rows + kTileKeys - 1) / kTileKeys : 0);
   }
   std::vector<size_t> order(units.size());
   std::iota(order.begin(), order.end(), size_t{0});
   std::stable_sort(order.begin(), order.end(),
                    [&](size_t x, size_t y) { return cost[x] > cost[y]; });
 
-  const size_t bytes = sizeof(PlanHeader) + sizeof(AttnUnit) * units.size() +
-                       sizeof(MergeGroup) * merges.size();
+  const size_t bytes =
+      sizeof(PlanHeader) + sizeof(AttnUnit) * units.size() + sizeof(MergeGroup) * merges.size();
   *plan_bytes = bytes;
   *plan_units = static_cast<int32_t>(units.size());
   *plan_merges = static_cast<int32_t>(merges.size());
@@ -535,22 +764,26 @@ extern "C" int sg_tree_attn_fwd(const SgTreeAttnArgs* args, sg_stream_t stream) 
   SG_REQUIRE(a.q_row_stride % 8 == 0 && a.q_head_stride % 8 == 0 &&
                  a.cache_head_stride % 8 == 0 && a.cache_token_stride % 8 == 0 &&
                  a.tree_row_stride % 8 == 0 && a.tree_head_stride % 8 == 0 &&
-                 a.out_row_stride % 8 == 0 && a.out_head_stride % 8 == 0,
+                 a.out_row_stride % 4 == 0 && a.out_head_stride % 4 == 0,
              "strides must be multiples of 8 elements (16-byte rows)");
+  // Lane offsets inside one key tile are 32-bit byte offsets.
+  SG_REQUIRE(a.cache_token_stride >= 0 && a.cache_token_stride < (int64_t{1} << 24) &&
+                 a.tree_row_stride >= 0 && a.tree_row_stride < (int64_t{1} << 24),
+             "cache_token_stride and tree_row_stride must lie in [0, 2^24) elements");
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (a.head_dim == 128) {
-    hipLaunchKernelGGL(tree_attn_kernel<128>, dim3(a.plan_units), dim3(kAttnThreads), 0, s, a);
+    hipLaunchKernelGGL(tree_attn_kernel<128>, dim3(a.plan_units), dim3(kThreads), 0, s, a);
     SG_LAUNCH_CHECK();
     if (a.plan_merges > 0) {
-      hipLaunchKernelGGL(tree_attn_merge_kernel<128>, dim3(a.plan_merges), dim3(kAttnThreads),
+      hipLaunchKernelGGL(tree_attn_merge_kernel<128>, dim3(a.plan_merges), dim3(kMergeThreads),
                          0, s, a);
       SG_LAUNCH_CHECK();
     }
   } else {
-    hipLaunchKernelGGL(tree_attn_kernel<64>, dim3(a.plan_units), dim3(kAttnThreads), 0, s, a);
+    hipLaunchKernelGGL(tree_attn_kernel<64>, dim3(a.plan_units), dim3(kThreads), 0, s, a);
     SG_LAUNCH_CHECK();
     if (a.plan_merges > 0) {
-      hipLaunchKernelGGL(tree_attn_merge_kernel<64>, dim3(a.plan_merges), dim3(kAttnThreads),
+      hipLaunchKernelGGL(tree_attn_merge_kernel<64>, dim3(a.plan_merges), dim3(kMergeThreads),
                          0, s, a);
       SG_LAUNCH_CHECK();
     }

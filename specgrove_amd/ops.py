@@ -59,8 +59,11 @@ class AttnPlan:
     workspace: torch.Tensor | None = None
 
     def to(self, device) -> "AttnPlan":
+        """Copy the plan to the device and allocate its workspace (the fp32
+        partial results of split units; every slot is written before the merge
+        kernel reads it, so its initial contents do not matter)."""
         self.device = torch.from_numpy(self.host).to(device, non_blocking=False)
-        self.workspace = torch.empty(max(self.workspace_bytes, 16), dtype=torch.uint8,
+        self.workspace = torch.zeros(max(self.workspace_bytes, 16), dtype=torch.uint8,
                                      device=device)
         return self
 
@@ -91,13 +94,23 @@ def plan_attention(row_offset, prefix_len, num_q_heads: int, num_kv_heads: int,
                     num_kv_heads, head_dim)
 
 
+UNIT_FIELDS = ("req", "kv_head", "row_begin", "row_count", "key_begin", "key_end",
+               "partial", "flags", "group", "num_splits", "first_partial", "pad")
+
+
+MERGE_FIELDS = ("req", "kv_head", "row_begin", "row_count", "first_partial", "num_partials",
+                "pad0", "pad1")
+
+
 def decode_plan(plan: AttnPlan):
-    """(header, units [U, 8], merges [M, 8]) int32 views of a host plan."""
+    """(header [16], units [U, 12], merges [M, 8]) int32 views of a host plan;
+    unit columns are UNIT_FIELDS, merge-group columns MERGE_FIELDS."""
     words = plan.host.view(np.int32)
     header = words[:16]
-    units = words[16:16 + 8 * plan.units].reshape(plan.units, 8)
-    merges = words[16 + 8 * plan.units:16 + 8 * (plan.units + plan.merges)].reshape(
-        plan.merges, 8)
+    end = 16 + len(UNIT_FIELDS) * plan.units
+    units = words[16:end].reshape(plan.units, len(UNIT_FIELDS))
+    merges = words[end:end + len(MERGE_FIELDS) * plan.merges].reshape(plan.merges,
+                                                                       len(MERGE_FIELDS))
     return header, units, merges
 
 

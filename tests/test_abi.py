@@ -38,28 +38,42 @@ def _check_plan(wl, target):
     assert header[0] == 0x53475041 and header[1] == plan.units and header[2] == plan.merges
     rows_per_tile = 128 // (wl.num_q_heads // wl.num_kv_heads)
     cover = {}
-    for req, g, row_begin, row_count, kb, ke, partial, flags in units.tolist():
-        key = (req, g, row_begin)
+    for (req, g, row_begin, row_count, kb, ke, partial, flags, group, splits, first,
+         _) in units.tolist():
         assert row_begin % rows_per_tile == 0
         assert row_count == min(rows_per_tile, int(wl.rows[req]) - row_begin)
-        cover.setdefault(key, []).append((kb, ke, partial, flags))
+        cover.setdefault((req, g, row_begin), []).append(
+            (kb, ke, partial, flags, group, splits, first))
+    groups = {}
     for req in range(wl.num_requests):
         for g in range(wl.num_kv_heads):
             for row_begin in range(0, int(wl.rows[req]), rows_per_tile):
                 parts = sorted(cover.pop((req, g, row_begin)))
                 assert parts[0][0] == 0 and parts[-1][1] == int(wl.prefix_len[req])
-                for (a0, a1, _, _), (b0, _, _, _) in zip(parts, parts[1:]):
-                    assert a1 == b0 and a0 < a1
-                assert sum(f & 1 for *_, f in parts) == 1
+                for a, b in zip(parts, parts[1:]):
+                    assert a[1] == b[0] and a[0] < a[1]
+                assert sum(p[3] & 1 for p in parts) == 1 and parts[-1][3] & 1
+                assert all(p[5] == len(parts) for p in parts)
                 if len(parts) == 1:
-                    assert parts[0][2] == -1
+                    assert parts[0][2] == -1 and parts[0][4] == -1
                 else:
-                    assert all(p >= 0 for _, _, p, _ in parts)
+                    assert len({p[4] for p in parts}) == 1
+                    slots = sorted(p[2] for p in parts)
+                    assert slots == list(range(parts[0][6], parts[0][6] + len(parts)))
+                    groups[parts[0][4]] = (req, g, row_begin,
+                                           min(rows_per_tile, int(wl.rows[req]) - row_begin),
+                                           parts[0][6], len(parts))
     assert not cover
-    slots = sorted(int(p) for p in units[:, 6] if p >= 0)
-    assert slots == list(range(len(slots)))
-    assert sum(int(m[5]) for m in merges) == len(slots)
-    assert plan.workspace_bytes == len(slots) * 128 * (wl.head_dim + 2) * 4
+    assert sorted(groups) == list(range(plan.merges))
+    for k, rec in enumerate(merges.tolist()):
+        assert tuple(rec[:6]) == groups[k]
+    partials = int(header[6])
+    assert partials == sum(1 for u in units if u[6] >= 0)
+    assert plan.workspace_bytes == partials * 128 * (wl.head_dim + 2) * 4
+    # Longest units first.
+    cost = [(u[5] - u[4] + 63) // 64 + ((int(wl.rows[u[0]]) + 63) // 64 if u[7] & 1 else 0)
+            for u in units.tolist()]
+    assert cost == sorted(cost, reverse=True)
     return plan
 
 
