@@ -46,6 +46,10 @@ def parse_args():
     p.add_argument("--cpu-requests", type=int, default=16,
                    help="requests in the CPU baseline's dense packed sample")
     p.add_argument("--target-units", type=int, default=0)
+    p.add_argument("--counters-only", action="store_true",
+                   help="for hardware-counter runs: --steps attention calls on the rotating "
+                        "input sets, then one 1 GiB device copy whose counter readings "
+                        "calibrate FETCH_SIZE / WRITE_SIZE; prints nothing")
     return p.parse_args()
 
 
@@ -195,6 +199,19 @@ def read_traffic():
         return None
 
 
+def counters_only(torch, np, W, ops, device, steps, warmup):
+    """Attention calls plus a copy of known size, for rocprofv3 --pmc runs."""
+    wl, plan, meta, sets = build_attention_sets(torch, np, W, ops, device, 4)
+    for k in range(warmup + steps):
+        attention_call(ops, wl, plan, meta, sets[k % N_SETS])
+    torch.cuda.synchronize()
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=device).fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -211,6 +228,9 @@ def main():
     device = torch.device("cuda:0")
     torch.cuda.init()
     steps, warmup = args.steps, args.warmup
+    if args.counters_only:
+        counters_only(torch, np, W, ops, device, steps, warmup)
+        return
     wl, plan, meta, sets = build_attention_sets(torch, np, W, ops, device,
                                                 3 * (steps + warmup) + 16)
     rows = wl.total_rows
@@ -242,7 +262,7 @@ def main():
     commit_avg = statistics.fmean(commit_ms)
 
     result = {
-        "metric": "packed-verify rows/s at Qwen3-8B shape",
+        "metric": "packed-verify rows/s at Qwen3-8B shape; % HBM roofline; tree-sample nodes/s",
         "value": rows / (ms_per_step * 1e-3),
         "unit": "rows/s",
         "n_gpus": 1,
