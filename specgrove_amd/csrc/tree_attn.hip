@@ -188,13 +188,15 @@ __global__ __launch_bounds__(kThreads, 1) void tree_attn_kernel(SgTreeAttnArgs a
   constexpr int DB = D / 32;                     // PV blocks of 32 head dims
   constexpr int ROWB = D * 2;                    // bytes per unpadded K/V row
   constexpr int STAGEB = kTileKeys * ROWB;       // bytes of one K (or V) tile
+  constexpr int CHUNKS = ROWB / 16;              // 16-byte chunks per row
   constexpr int ROWS_PER_KB = 1024 / ROWB;       // rows covered by one wave DMA
   constexpr int DMAS = STAGEB / 1024 / kWaves;   // DMAs per wave per K (or V) tile
   constexpr int STATE = 2 + 16 * DB;             // floats per lane of a WaveState
   static_assert(DMAS >= 1, "tile too small for the workgroup");
+  static_assert(kStages == 4, "the issue schedule assumes a 4-tile ring");
   static_assert(kStages * STAGEB <= 65536, "ring offsets must fit the LDS immediate");
   static_assert(2 * kStages * STAGEB >= 6 * STATE * 64 * 4, "merge scratch");
-  // Ring of kStages tiles of K and of V; reused as the merge scratch at the end.
+  // Rings of kStages tiles of K and of V; reused as the merge scratch at the end.
   __shared__ __align__(1024) unsigned char s_k[kStages * STAGEB];
   __shared__ __align__(1024) unsigned char s_v[kStages * STAGEB];
   __shared__ uint32_t s_anc[kQPerUnit][kAncWords];
@@ -209,16 +211,18 @@ __global__ __launch_bounds__(kThreads, 1) void tree_attn_kernel(SgTreeAttnArgs a
   const int half = lane >> 5;
   const int col = lane & 31;
   const int nq = (u.row_count * G + 31) / 32;   // q-groups in use, 1..4
-  // Waves sharing a q-group: 4 when the unit has 1-2 q-groups (they take the
-  // four 32-key blocks of two consecutive tiles), else 2 (the two blocks of one
-  // tile).  Either way every wave handles one 32-key block per iteration.
+  // Waves sharing a q-group ("key streams"): 4 when the unit has 1-2 q-groups
+  // (they take the four 32-key blocks of two consecutive tiles), else 2 (the
+  // two blocks of one tile).  Every wave handles one 32-key block per
+  // iteration.  Waves beyond nq*streams repeat stream 0's work on the same
+  // LDS data and discard it.
   const int streams = nq <= 2 ? 4 : 2;
   const int per_iter = streams / 2;             // tiles consumed per iteration
   const int qg = wave % nq;
   const int ks = wave / nq;                     // key stream of this wave
   const bool active = ks < streams;
-  const int my_tile = ks >> 1;                  // tile of the iteration this wave takes
-  const int my_blk = ks & 1;                    // 32-key block inside that tile
+  const int my_tile = active ? (ks >> 1) : 0;   // tile of the iteration this wave takes
+  const int my_blk = active ? (ks & 1) : 0;     // 32-key block inside that tile
   const int m = qg * 32 + col;                  // query vector inside the unit
   const int r_local = m / G;                    // query row inside the tile
   const int head = u.kv_head * G + (m - r_local * G);
@@ -279,62 +283,98 @@ __global__ __launch_bounds__(kThreads, 1) void tree_attn_kernel(SgTreeAttnArgs a
                        static_cast<int64_t>(r0) * a.tree_row_stride;
 
   // DMA slots of this lane: wave DMA i of a tile covers LDS rows
-  // ROWS_PER_KB*(wave*DMAS + i) + lane / (ROWB/16), physical chunk lane % (ROWB/16);
+  // ROWS_PER_KB*(wave*DMAS + i) + lane / CHUNKS, physical chunk lane % CHUNKS;
   // the row holds key pi(row) for K and key row for V.  Full prefix tiles use
   // precomputed lane offsets; the last partial tile and tree tiles clamp the key.
   const int cstride = static_cast<int>(a.cache_token_stride);
+  const int tstride = static_cast<int>(a.tree_row_stride);
   uint32_t k_dma[DMAS], v_dma[DMAS];
 #pragma unroll
   for (int i = 0; i < DMAS; ++i) {
-    const int lds_row = ROWS_PER_KB * (wave * DMAS + i) + lane / (ROWB / 16);
-    const int phys = lane % (ROWB / 16);
+    const int lds_row = ROWS_PER_KB * (wave * DMAS + i) + lane / CHUNKS;
+    const int phys = lane % CHUNKS;
     const int kk = (lds_row & ~31) + key_pi(lds_row & 31);
     k_dma[i] = static_cast<uint32_t>(2 * (kk * cstride + 8 * (phys ^ swz_k<D>(lds_row))));
     v_dma[i] = static_cast<uint32_t>(2 * (lds_row * cstride + 8 * (phys ^ swz_v<D>(lds_row))));
   }
-  auto load_tile = [&](int t) {
-    if (t >= tiles) return;
-    const int stage = t % kStages;
-    const uint32_t kdst = lds_addr(s_k + stage * STAGEB + wave * DMAS * 1024);
-    const uint32_t vdst = lds_addr(s_v + stage * STAGEB + wave * DMAS * 1024);
+  // K (is_v false) or V half of tile t into ring stage t % kStages.
+  auto load_half = [&](int t, bool is_v) {
+    unsigned char* ring = is_v ? s_v : s_k;
+    const uint32_t dst = lds_addr(ring + (t % kStages) * STAGEB + wave * DMAS * 1024);
     if (t < tiles_full) {
-      const unsigned char* kb0 =
-          reinterpret_cast<const unsigned char*>(kc + static_cast<int64_t>(t) * kTileKeys * cstride);
-      const unsigned char* vb0 =
-          reinterpret_cast<const unsigned char*>(vc + static_cast<int64_t>(t) * kTileKeys * cstride);
+      const unsigned char* base = reinterpret_cast<const unsigned char*>(
+          (is_v ? vc : kc) + static_cast<int64_t>(t) * kTileKeys * cstride);
 #pragma unroll
-      for (int i = 0; i < DMAS; ++i) {
-        dma16(kb0, k_dma[i], kdst + 1024 * i);
-        dma16(vb0, v_dma[i], vdst + 1024 * i);
-      }
+      for (int i = 0; i < DMAS; ++i) dma16(base, is_v ? v_dma[i] : k_dma[i], dst + 1024 * i);
       return;
     }
     const bool tree = t >= tiles_prefix;
     const int key0 = tree ? (t - tiles_prefix) * kTileKeys : t * kTileKeys;
     const int last = (tree ? n : prefix_keys) - key0 - 1;
-    const int stride = tree ? static_cast<int>(a.tree_row_stride) : cstride;
-    const unsigned char* kb0 = reinterpret_cast<const unsigned char*>(
-        (tree ? kt : kc) + static_cast<int64_t>(key0) * stride);
-    const unsigned char* vb0 = reinterpret_cast<const unsigned char*>(
-        (tree ? vt : vc) + static_cast<int64_t>(key0) * stride);
+    const int stride = tree ? tstride : cstride;
+    const uint16_t* src = tree ? (is_v ? vt : kt) : (is_v ? vc : kc);
+    const unsigned char* base =
+        reinterpret_cast<const unsigned char*>(src + static_cast<int64_t>(key0) * stride);
 #pragma unroll
     for (int i = 0; i < DMAS; ++i) {
-      const int lds_row = ROWS_PER_KB * (wave * DMAS + i) + lane / (ROWB / 16);
-      const int phys = lane % (ROWB / 16);
+      const int lds_row = ROWS_PER_KB * (wave * DMAS + i) + lane / CHUNKS;
+      const int phys = lane % CHUNKS;
       // Keys past the range re-read the last valid key: finite data that the
       // score mask (K) or a zero probability (V) removes.
-      const int kk = min((lds_row & ~31) + key_pi(lds_row & 31), last);
-      const int vk = min(lds_row, last);
-      dma16(kb0, static_cast<uint32_t>(2 * (kk * stride + 8 * (phys ^ swz_k<D>(lds_row)))),
-            kdst + 1024 * i);
-      dma16(vb0, static_cast<uint32_t>(2 * (vk * stride + 8 * (phys ^ swz_v<D>(lds_row)))),
-            vdst + 1024 * i);
+      const int key = is_v ? min(lds_row, last) : min((lds_row & ~31) + key_pi(lds_row & 31), last);
+      const int sw = is_v ? swz_v<D>(lds_row) : swz_k<D>(lds_row);
+      dma16(base, static_cast<uint32_t>(2 * (key * stride + 8 * (phys ^ sw))), dst + 1024 * i);
     }
   };
 
+  // Issue schedule.  Iterations ("windows", one barrier each) i = 0 ..
+  // groups-1 each consume one group of per_iter tiles: the PV products of
+  // group i and the QK products of group i+1 (one group ahead, so that the QK
+  // MFMAs overlap the softmax VALU work).  Window j issues the V tiles of
+  // group j+lv and then the K tiles of group j+lk.
+  //   per_iter 1: lk 4, lv 2.  The waves of key stream 1 run half a window
+  //     behind stream 0 (PV of group i-1 first, then the QK/softmax of group
+  //     i), so the two waves sharing a SIMD alternate between MFMA-heavy and
+  //     VALU/LDS-heavy phases.  Window i reads K(i+1), V(i) and V(i-1); the
+  //     ring keeps 2.5 tiles in flight.
+  //   per_iter 2: lk 2, lv 1, no lag; one group (two tiles) in flight.
+  const int groups = (tiles + per_iter - 1) / per_iter;
+  const bool pingpong = per_iter == 1;
+  const bool lag = pingpong && ks == 1;
+  const int lk = kStages / per_iter;
+  const int lv = pingpong ? 2 : 1;
+  auto group_tiles = [&](int grp) {
+    return grp < 0 ? 0 : max(0, min(per_iter, tiles - grp * per_iter));
+  };
+  auto issue = [&](int j) {
+    const int nv = group_tiles(j + lv);
+    for (int k = 0; k < nv; ++k) load_half((j + lv) * per_iter + k, true);
+    const int nk = group_tiles(j + lk);
+    for (int k = 0; k < nk; ++k) load_half((j + lk) * per_iter + k, false);
+  };
+  // Wait until at most `newer` half tiles (the newest ones) are in flight.
+  auto wait_halves = [&](int newer) {
+    switch (newer) {
+      case 0: __builtin_amdgcn_s_waitcnt(vmcnt_encoding(0)); break;
+      case 1: __builtin_amdgcn_s_waitcnt(vmcnt_encoding(DMAS)); break;
+      case 2: __builtin_amdgcn_s_waitcnt(vmcnt_encoding(2 * DMAS)); break;
+      case 3: __builtin_amdgcn_s_waitcnt(vmcnt_encoding(3 * DMAS)); break;
+      case 4: __builtin_amdgcn_s_waitcnt(vmcnt_encoding(4 * DMAS)); break;
+      default: __builtin_amdgcn_s_waitcnt(vmcnt_encoding(5 * DMAS)); break;
+    }
+  };
+  // Window i needs V(i) (issued first in window i-lv) and K(i+1) (issued last
+  // in window i+1-lk).  per_iter 1: V(i) is the later one; K(i+2) of window
+  // i-2 and all of window i-1 may still be in flight.  per_iter 2: both come
+  // from window i-1, the latest window, so nothing may be in flight.
+  auto newer_before = [&](int i) {
+    if (!pingpong) return 0;
+    return group_tiles(i + 2) + group_tiles(i + 1) + group_tiles(i + 3);
+  };
+
   // Lane parts of the LDS read addresses (bytes), including this wave's tile
-  // offset inside the iteration and its block inside the tile; the ring stage
-  // is a compile-time immediate.
+  // offset inside its group (my_tile stages) and its block inside the tile;
+  // callers pass the ring stage of the group's first tile.
   const int gq = lane >> 4;
   const int jj = lane & 15;
   const int rr = jj >> 2;
@@ -364,36 +404,26 @@ __global__ __launch_bounds__(kThreads, 1) void tree_attn_kernel(SgTreeAttnArgs a
 #pragma unroll
     for (int r = 0; r < 16; ++r) st.acc[db][r] = 0.0f;
 
-  // This wave's 32-key block of ring stage S: S^T, online softmax, O^T.
-  // key0 = first key of the block's tile (for masks), limit = keys in range.
-  auto compute = [&](auto stage_tag, auto mode_tag, int key0, int limit) {
-    constexpr int kStage = decltype(stage_tag)::value;
-    constexpr Mask kMode = decltype(mode_tag)::value;
-    const unsigned char* sk = s_k + kStage * STAGEB;
-    const unsigned char* sv = s_v + kStage * STAGEB;
-    float x[16];
-    {
-      floatx16 s;
+  // S^T of this wave's 32-key block of the group whose first tile is in ring
+  // stage `stage`.
+  auto qk = [&](int stage) {
+    const unsigned char* sk = s_k + stage * STAGEB;
+    floatx16 s;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[r] = 0.0f;
-      bf16x8 kf[KB];
+    for (int r = 0; r < 16; ++r) s[r] = 0.0f;
+    bf16x8 kf[KB];
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-        kf[kb] = as_bf16x8(*reinterpret_cast<const uint4*>(sk + k_off[kb]));
+    for (int kb = 0; kb < KB; ++kb)
+      kf[kb] = as_bf16x8(*reinterpret_cast<const uint4*>(sk + k_off[kb]));
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kb], qf[kb], s, 0, 0, 0);
-      const int first = key0 + 32 * my_blk + 16 * half;
-      uint32_t bits = 0xffffffffu;
-      if (kMode == Mask::kTree) bits = s_anc[r_local][(key0 + 32 * my_blk) >> 5] >> (16 * half);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        bool visible = true;
-        if (kMode != Mask::kFull) visible = first + r < limit;
-        if (kMode == Mask::kTree) visible = visible && ((bits >> r) & 1u);
-        x[r] = visible ? s[r] : -__builtin_inff();
-      }
-    }
+    for (int kb = 0; kb < KB; ++kb)
+      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kb], qf[kb], s, 0, 0, 0);
+    return s;
+  };
+  // Online softmax, step 1: new running max of the scores x (masked already);
+  // the state is rescaled only when some lane's max grew (rare after the
+  // first blocks).
+  auto softmax_max = [&](const float (&x)[16]) {
     float tmax = x[0];
 #pragma unroll
     for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, x[r]);
@@ -409,6 +439,10 @@ __global__ __launch_bounds__(kThreads, 1) void tree_attn_kernel(SgTreeAttnArgs a
         for (int r = 0; r < 16; ++r) st.acc[db][r] *= alpha;
       st.m = m_new;
     }
+  };
+  // Step 2: probabilities exp2((x - m) * c2) and their sum.  Independent of
+  // the accumulators, so it interleaves with the next block's QK MFMAs.
+  auto softmax_exp = [&](float (&x)[16]) {
     const float mc = (st.m == -__builtin_inff()) ? 0.0f : st.m * c2;
     float psum = 0.0f;
 #pragma unroll
@@ -417,11 +451,20 @@ __global__ __launch_bounds__(kThreads, 1) void tree_attn_kernel(SgTreeAttnArgs a
       psum += x[r];
     }
     st.l += half_sum(psum);
+  };
+  // Step 3: bf16 probabilities, in the B-operand layout of the PV MFMA (two
+  // 16-key halves).
+  auto pack = [&](const float (&x)[16], bf16x8 (&pf)[2]) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pf[c][e] = static_cast<__bf16>(x[8 * c + e]);
+  };
+  // Step 4: O^T += V^T P^T from ring stage `stage`.
+  auto pv = [&](const bf16x8 (&pf)[2], int stage) {
+    const unsigned char* sv = s_v + stage * STAGEB;
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      bf16x8 pf;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) pf[e] = static_cast<__bf16>(x[8 * c + e]);
       const unsigned char* vrows = sv + 8 * c * ROWB;
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
@@ -431,64 +474,125 @@ __global__ __launch_bounds__(kThreads, 1) void tree_attn_kernel(SgTreeAttnArgs a
             __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(vrows + v_off[db][1]));
         const short8_t both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         st.acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, both),
-                                                             pf, st.acc[db], 0, 0, 0);
+                                                             pf[c], st.acc[db], 0, 0, 0);
       }
     }
   };
 
-  // Pipeline: tiles t0 .. t0+per_iter-1 are computed while the next
-  // kStages-per_iter tiles stream in.  Each tile is DMAS K + DMAS V
-  // instructions per wave, so "everything but the newest j tiles has landed"
-  // is vmcnt(2*DMAS*j).
-  const int ahead = kStages - per_iter;
-  auto wait_tiles = [&](int newer) {
-    if (newer >= 2) {
-      __builtin_amdgcn_s_waitcnt(vmcnt_encoding(4 * DMAS));
-    } else if (newer == 1) {
-      __builtin_amdgcn_s_waitcnt(vmcnt_encoding(2 * DMAS));
-    } else {
-      __builtin_amdgcn_s_waitcnt(0);
-    }
-  };
-  for (int t = 0; t < ahead; ++t) load_tile(t);
-
-  // Iteration over tile groups t0 = per_iter*i.  The wave's tile is
-  // t0 + my_tile, in ring stage (t0 % kStages) + my_tile (no wrap: per_iter
-  // divides kStages and t0 is a multiple of per_iter).
-  auto iterate = [&](int t0, auto base_tag) {
-    constexpr int kBase = decltype(base_tag)::value;
-    const int issued = min(tiles, t0 + ahead);
-    wait_tiles(issued - min(tiles, t0 + per_iter));
-    __syncthreads();
-    for (int k = 0; k < per_iter; ++k) load_tile(t0 + ahead + k);
-    const int t = t0 + my_tile;
-    if (!active || t >= tiles) return;
-    if (t < tiles_full) {
-      compute(IntTag<kBase>{}, MaskTag<Mask::kFull>{}, 0, 0);
-    } else if (t < tiles_prefix) {
-      compute(IntTag<kBase>{}, MaskTag<Mask::kLimit>{}, t * kTileKeys, prefix_keys);
-    } else {
-      compute(IntTag<kBase>{}, MaskTag<Mask::kTree>{}, (t - tiles_prefix) * kTileKeys, n);
-    }
-  };
-  int t0 = 0;
-  if (per_iter == 1) {
-    for (; t0 + 4 <= tiles; t0 += 4) {
-      iterate(t0, IntTag<0>{});
-      iterate(t0 + 1, IntTag<1>{});
-      iterate(t0 + 2, IntTag<2>{});
-      iterate(t0 + 3, IntTag<3>{});
-    }
-    if (t0 < tiles) iterate(t0++, IntTag<0>{});
-    if (t0 < tiles) iterate(t0++, IntTag<1>{});
-    if (t0 < tiles) iterate(t0++, IntTag<2>{});
+  // Prologue: windows -lk .. -1 of the issue schedule, then QK of group 0,
+  // which needs K(0) from window -lk; everything issued after it may be in
+  // flight: V(0), V(1), K(1), K(2), K(3) (per_iter 1) or V(0), K(1) (per_iter 2).
+  for (int j = -lk; j < 0; ++j) issue(j);
+  if (pingpong) {
+    wait_halves(group_tiles(0) + group_tiles(1) + group_tiles(1) + group_tiles(2) +
+                group_tiles(3));
   } else {
-    for (; t0 + 4 <= tiles; t0 += 4) {
-      iterate(t0, IntTag<0>{});
-      iterate(t0 + 2, IntTag<2>{});
+    wait_halves(group_tiles(0) + group_tiles(1));
+  }
+  __syncthreads();
+  floatx16 s_next;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) s_next[r] = 0.0f;
+  if (my_tile < tiles) s_next = qk(0);
+
+  auto window = [&](int i) {
+    wait_halves(newer_before(i));
+    __syncthreads();
+    issue(i);
+  };
+  // Softmax of the current block interleaved with the next block's QK MFMAs;
+  // leaves the probabilities in pf.
+  auto softmax_qk = [&](int next_stage, bf16x8 (&pf)[2]) {
+    float x[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) x[r] = s_next[r];
+    softmax_max(x);
+    s_next = qk(next_stage);
+    softmax_exp(x);
+    __builtin_amdgcn_sched_group_barrier(0x100, KB, 0);
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
     }
-    if (t0 < tiles) iterate(t0, IntTag<0>{});
-    if (t0 + 2 < tiles) iterate(t0 + 2, IntTag<2>{});
+    pack(x, pf);
+  };
+
+  // Steady state: windows whose current and next tiles are full prefix tiles
+  // need no mask, and the ring stages are compile-time constants in loops
+  // unrolled by the ring size.  Every tile of groups i and i+1 is full for
+  // i < steady_end.
+  const int steady_end = max(0, tiles_full / per_iter - 1);
+  int i = 0;
+  bf16x8 pf[2];
+  if (!pingpong) {
+    auto step = [&](int w, auto cur_tag, auto next_tag) {
+      window(w);
+      softmax_qk(decltype(next_tag)::value, pf);
+      pv(pf, decltype(cur_tag)::value);
+    };
+    for (; i + 2 <= steady_end; i += 2) {
+      step(i, IntTag<0>{}, IntTag<2>{});
+      step(i + 1, IntTag<2>{}, IntTag<0>{});
+    }
+  } else if (!lag) {
+    auto step = [&](int w, auto cur_tag) {
+      constexpr int kCur = decltype(cur_tag)::value;
+      window(w);
+      softmax_qk((kCur + 1) % kStages, pf);
+      pv(pf, kCur);
+    };
+    for (; i + 4 <= steady_end; i += 4) {
+      step(i, IntTag<0>{});
+      step(i + 1, IntTag<1>{});
+      step(i + 2, IntTag<2>{});
+      step(i + 3, IntTag<3>{});
+    }
+  } else if (steady_end > 0) {
+    // Lagging stream: PV of the previous window's probabilities first.
+    auto step = [&](int w, auto cur_tag) {
+      constexpr int kCur = decltype(cur_tag)::value;
+      window(w);
+      pv(pf, (kCur + kStages - 1) % kStages);
+      softmax_qk((kCur + 1) % kStages, pf);
+    };
+    window(0);
+    softmax_qk(1, pf);
+    i = 1;
+    for (; i + 4 <= steady_end; i += 4) {
+      step(i, IntTag<1>{});
+      step(i + 1, IntTag<2>{});
+      step(i + 2, IntTag<3>{});
+      step(i + 3, IntTag<0>{});
+    }
+    // Catch up before the unlagged windows: PV of window i-1 (its V tile stays
+    // in the ring until window i+1 issues).
+    pv(pf, (i - 1) % kStages);
+  }
+  // Remaining windows: runtime stages, masks from the key limit and the
+  // ancestor bitsets.
+  for (; i < groups; ++i) {
+    window(i);
+    const int t = i * per_iter + my_tile;
+    const int t_next = t + per_iter;
+    float x[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) x[r] = s_next[r];
+    if (t_next < tiles) s_next = qk(((i + 1) * per_iter) % kStages);
+    if (t < tiles) {
+      const bool tree = t >= tiles_prefix;
+      const int key0 = (tree ? t - tiles_prefix : t) * kTileKeys + 32 * my_blk;
+      const int limit = tree ? n : prefix_keys;
+      const uint32_t bits = tree ? (s_anc[r_local][key0 >> 5] >> (16 * half)) : 0xffffffffu;
+      const int first = key0 + 16 * half;
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        x[r] = (first + r < limit && ((bits >> r) & 1u)) ? x[r] : -__builtin_inff();
+      softmax_max(x);
+      softmax_exp(x);
+      pack(x, pf);
+      pv(pf, (i * per_iter) % kStages);
+    }
   }
   __syncthreads();
 
