@@ -82,7 +82,7 @@ typedef struct SgTreeAttnArgs {
   int64_t out_row_stride, out_head_stride;
   /* work plan from sg_tree_attn_plan (device copy) and its scratch */
   const void* plan_dev;
-  int32_t plan_units;    /* work units (first kernel's grid) */
+  int32_t plan_units;    /* work lists = workgroups of the first kernel */
   int32_t plan_merges;   /* split-K merge groups (second kernel's grid) */
   void* workspace_dev;
   size_t workspace_bytes;
@@ -90,9 +90,12 @@ typedef struct SgTreeAttnArgs {
 
 /* Host-side planner.  From host copies of row_offset [n+1] and prefix_len [n]
  * it writes the work list (plan_capacity_bytes of host memory) and reports its
- * size, unit count and the scratch bytes sg_tree_attn_fwd needs.  Replaces the
+ * size, its number of work lists (*plan_units: workgroups of the attention
+ * kernel, at most target_units_hint or 256, each a list of units packed by
+ * estimated cost), its split-merge groups and the scratch bytes
+ * sg_tree_attn_fwd needs.  Replaces the
  * host index lists the reference builds per wave (CTBD:327-350, :513-545).
- * target_units_hint <= 0 lets the planner size splits for 256 CUs. */
+ * target_units_hint <= 0 sizes the work lists and splits for 256 CUs. */
 int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset_host,
                       const int32_t* prefix_len_host, int32_t num_q_heads,
                       int32_t num_kv_heads, int32_t head_dim,

@@ -67,7 +67,8 @@ struct PlanHeader {
   int32_t head_dim;
   int32_t group;
   int32_t num_partials;
-  int32_t reserved[9];
+  int32_t num_bins;       // work lists = workgroups of the attention kernel
+  int32_t reserved[8];
 };
 static_assert(sizeof(PlanHeader) == 64, "plan header is 64 bytes");
 
@@ -182,8 +183,9 @@ struct WaveState {
   floatx16 acc[D / 32];
 };
 
+// Attention of one work unit by the whole workgroup.
 template <int D>
-__global__ __launch_bounds__(kThreads, 1) void tree_attn_kernel(SgTreeAttnArgs a) {
+__device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUnit& u) {
   constexpr int KB = D / 16;                     // QK^T k-blocks of 16 head dims
   constexpr int DB = D / 32;                     // PV blocks of 32 head dims
   constexpr int ROWB = D * 2;                    // bytes per unpadded K/V row
@@ -202,8 +204,6 @@ __global__ __launch_bounds__(kThreads, 1) void tree_attn_kernel(SgTreeAttnArgs a
   __shared__ uint32_t s_anc[kQPerUnit][kAncWords];
   __shared__ int s_parent[kMaxTreeRows];
 
-  const PlanHeader* hdr = static_cast<const PlanHeader*>(a.plan_dev);
-  const AttnUnit u = reinterpret_cast<const AttnUnit*>(hdr + 1)[blockIdx.x];
   const int G = a.num_q_heads / a.num_kv_heads;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -672,6 +672,22 @@ __global__ __launch_bounds__(kThreads, 1) void tree_attn_kernel(SgTreeAttnArgs a
     }
 }
 
+// One workgroup per work list (one per CU): the units of list b are
+// units[bin_offset[b] .. bin_offset[b+1]), processed in order.
+template <int D>
+__global__ __launch_bounds__(kThreads, 1) void tree_attn_kernel(SgTreeAttnArgs a) {
+  const PlanHeader* hdr = static_cast<const PlanHeader*>(a.plan_dev);
+  const AttnUnit* units = reinterpret_cast<const AttnUnit*>(hdr + 1);
+  const int32_t* bin_offset = reinterpret_cast<const int32_t*>(
+      reinterpret_cast<const MergeGroup*>(units + hdr->num_units) + hdr->num_merges);
+  const int end = bin_offset[blockIdx.x + 1];
+  for (int k = bin_offset[blockIdx.x]; k < end; ++k) {
+    const AttnUnit u = units[k];
+    attn_unit<D>(a, u);
+    __syncthreads();  // LDS of this unit is free before the next one starts
+  }
+}
+
 // Combines the partials of one split group: thread -> (query vector, float4 chunk).
 template <int D>
 __global__ __launch_bounds__(kMergeThreads) void tree_attn_merge_kernel(SgTreeAttnArgs a) {
@@ -813,22 +829,65 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
       }
     }
   }
-  // Longest units first: workgroups are dispatched in grid order.
+  // Work lists: units are packed onto `target` workgroups (one per CU) by
+  // longest-processing-time-first greedy assignment to the least-loaded list.
+  // Unit cost (hundredths of a microsecond on MI355X at 32q/8kv, D=128): a
+  // fixed part (prologue latency, epilogue) plus a per-64-key-tile part; a
+  // unit with at most two q-groups (64 query vectors) streams two tiles per
+  // window and costs less per tile.
   std::vector<int64_t> cost(units.size());
   for (size_t k = 0; k < units.size(); ++k) {
     const int rows = row_offset_host[units[k].req + 1] - row_offset_host[units[k].req];
-    cost[k] = (units[k].key_end - units[k].key_begin + kTileKeys - 1) / kTileKeys +
-              ((units[k].flags & 1) ? (rows + kTileKeys - 1) / kTileKeys : 0);
+    const int64_t tiles =
+        (units[k].key_end - units[k].key_begin + kTileKeys - 1) / kTileKeys +
+        ((units[k].flags & 1) ? (rows + kTileKeys - 1) / kTileKeys : 0);
+    const int nq = (units[k].row_count * G + 31) / 32;
+    cost[k] = nq <= 2 ? 550 + 114 * tiles : 840 + 175 * tiles;
   }
   std::vector<size_t> order(units.size());
   std::iota(order.begin(), order.end(), size_t{0});
   std::stable_sort(order.begin(), order.end(),
                    [&](size_t x, size_t y) { return cost[x] > cost[y]; });
+  const int64_t bins = std::min<int64_t>(target, static_cast<int64_t>(units.size()));
+  std::vector<int64_t> load(bins, 0);
+  std::vector<std::vector<size_t>> bin_units(bins);
+  for (size_t k : order) {
+    const int64_t b = std::min_element(load.begin(), load.end()) - load.begin();
+    load[b] += cost[k];
+    bin_units[b].push_back(k);
+  }
+  // Local search: move a unit out of the most loaded list, or swap it with a
+  // smaller unit of the least loaded list, while that lowers the maximum.
+  for (int round = 0; bins > 1 && round < 4096; ++round) {
+    const int64_t hi = std::max_element(load.begin(), load.end()) - load.begin();
+    const int64_t lo = std::min_element(load.begin(), load.end()) - load.begin();
+    const int64_t gap = load[hi] - load[lo];
+    int64_t best = 0;
+    size_t bi = 0, bj = SIZE_MAX;
+    for (size_t x = 0; x < bin_units[hi].size(); ++x) {
+      const int64_t cx = cost[bin_units[hi][x]];
+      if (cx < gap && cx > best) best = cx, bi = x, bj = SIZE_MAX;  // move
+      for (size_t y = 0; y < bin_units[lo].size(); ++y) {
+        const int64_t d = cx - cost[bin_units[lo][y]];
+        if (d > 0 && d < gap && d > best) best = d, bi = x, bj = y;  // swap
+      }
+    }
+    if (best == 0) break;
+    const size_t ux = bin_units[hi][bi];
+    if (bj == SIZE_MAX) {
+      bin_units[hi].erase(bin_units[hi].begin() + bi);
+      bin_units[lo].push_back(ux);
+    } else {
+      std::swap(bin_units[hi][bi], bin_units[lo][bj]);
+    }
+    load[hi] -= best;
+    load[lo] += best;
+  }
 
-  const size_t bytes =
-      sizeof(PlanHeader) + sizeof(AttnUnit) * units.size() + sizeof(MergeGroup) * merges.size();
+  const size_t bytes = sizeof(PlanHeader) + sizeof(AttnUnit) * units.size() +
+                       sizeof(MergeGroup) * merges.size() + sizeof(int32_t) * (bins + 1);
   *plan_bytes = bytes;
-  *plan_units = static_cast<int32_t>(units.size());
+  *plan_units = static_cast<int32_t>(bins);
   *plan_merges = static_cast<int32_t>(merges.size());
   *workspace_bytes = sizeof(float) * partial_floats(head_dim) * static_cast<size_t>(partials);
   if (plan_host == nullptr) return SG_OK;  // size query
@@ -841,11 +900,19 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
   hdr.head_dim = head_dim;
   hdr.group = G;
   hdr.num_partials = partials;
+  hdr.num_bins = static_cast<int32_t>(bins);
   char* out = static_cast<char*>(plan_host);
   std::memcpy(out, &hdr, sizeof(hdr));
   AttnUnit* uo = reinterpret_cast<AttnUnit*>(out + sizeof(hdr));
-  for (size_t k = 0; k < order.size(); ++k) uo[k] = units[order[k]];
-  std::memcpy(uo + units.size(), merges.data(), sizeof(MergeGroup) * merges.size());
+  MergeGroup* mo = reinterpret_cast<MergeGroup*>(uo + units.size());
+  int32_t* bo = reinterpret_cast<int32_t*>(mo + merges.size());
+  size_t next = 0;
+  for (int64_t b = 0; b < bins; ++b) {
+    bo[b] = static_cast<int32_t>(next);
+    for (size_t k : bin_units[b]) uo[next++] = units[k];
+  }
+  bo[bins] = static_cast<int32_t>(next);
+  std::memcpy(mo, merges.data(), sizeof(MergeGroup) * merges.size());
   return SG_OK;
 }
 

@@ -103,15 +103,19 @@ MERGE_FIELDS = ("req", "kv_head", "row_begin", "row_count", "first_partial", "nu
 
 
 def decode_plan(plan: AttnPlan):
-    """(header [16], units [U, 12], merges [M, 8]) int32 views of a host plan;
-    unit columns are UNIT_FIELDS, merge-group columns MERGE_FIELDS."""
+    """(header [16], units [U, 12], merges [M, 8], bin_offset [B+1]) int32 views
+    of a host plan; unit columns are UNIT_FIELDS, merge-group columns
+    MERGE_FIELDS.  Work list b (workgroup b of the attention kernel) runs
+    units[bin_offset[b]:bin_offset[b+1]]."""
     words = plan.host.view(np.int32)
     header = words[:16]
-    end = 16 + len(UNIT_FIELDS) * plan.units
-    units = words[16:end].reshape(plan.units, len(UNIT_FIELDS))
-    merges = words[end:end + len(MERGE_FIELDS) * plan.merges].reshape(plan.merges,
-                                                                       len(MERGE_FIELDS))
-    return header, units, merges
+    n_units, n_merges, n_bins = int(header[1]), int(header[2]), int(header[7])
+    end = 16 + len(UNIT_FIELDS) * n_units
+    units = words[16:end].reshape(n_units, len(UNIT_FIELDS))
+    mend = end + len(MERGE_FIELDS) * n_merges
+    merges = words[end:mend].reshape(n_merges, len(MERGE_FIELDS))
+    bins = words[mend:mend + n_bins + 1]
+    return header, units, merges, bins
 
 
 def tree_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,

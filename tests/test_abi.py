@@ -34,8 +34,11 @@ def test_every_declared_symbol_is_exported():
 def _check_plan(wl, target):
     plan = ops.plan_attention(wl.row_offset, wl.prefix_len, wl.num_q_heads, wl.num_kv_heads,
                               wl.head_dim, target)
-    header, units, merges = ops.decode_plan(plan)
-    assert header[0] == 0x53475041 and header[1] == plan.units and header[2] == plan.merges
+    header, units, merges, bins = ops.decode_plan(plan)
+    assert header[0] == 0x53475041 and header[2] == plan.merges
+    # work lists: one per workgroup, contiguous, covering every unit once
+    assert header[7] == plan.units == min(target if target > 0 else 256, len(units))
+    assert bins[0] == 0 and bins[-1] == len(units) and (np.diff(bins) >= 1).all()
     rows_per_tile = 128 // (wl.num_q_heads // wl.num_kv_heads)
     cover = {}
     for (req, g, row_begin, row_count, kb, ke, partial, flags, group, splits, first,
@@ -70,10 +73,14 @@ def _check_plan(wl, target):
     partials = int(header[6])
     assert partials == sum(1 for u in units if u[6] >= 0)
     assert plan.workspace_bytes == partials * 128 * (wl.head_dim + 2) * 4
-    # Longest units first.
-    cost = [(u[5] - u[4] + 63) // 64 + ((int(wl.rows[u[0]]) + 63) // 64 if u[7] & 1 else 0)
-            for u in units.tolist()]
-    assert cost == sorted(cost, reverse=True)
+    # Balanced lists: no list exceeds the mean load by more than its largest unit.
+    def cost(u):
+        tiles = (u[5] - u[4] + 63) // 64 + ((int(wl.rows[u[0]]) + 63) // 64 if u[7] & 1 else 0)
+        nq = (u[3] * (wl.num_q_heads // wl.num_kv_heads) + 31) // 32
+        return 550 + 114 * tiles if nq <= 2 else 840 + 175 * tiles
+    costs = [cost(u) for u in units.tolist()]
+    loads = [sum(costs[bins[b]:bins[b + 1]]) for b in range(len(bins) - 1)]
+    assert max(loads) <= sum(costs) / len(loads) + max(costs)
     return plan
 
 
