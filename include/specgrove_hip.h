@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define SG_ABI_VERSION 1
+#define SG_ABI_VERSION 2
 
 #define SG_OK 0
 #define SG_EINVAL (-1)  /* shape or contract violation (Python: ValueError) */
@@ -175,10 +175,17 @@ typedef struct SgTreeSampleArgs {
   int32_t* bonus_dev;            /* [n] */
   int32_t* keep_rows_dev;        /* optional [n, max_depth+1]: [0] + nodes, -1 padded */
   int32_t* status_dev;           /* optional [1]: SG_EINVAL if a walk broke the contract */
+  void* workspace_dev;           /* >= sg_tree_sample_workspace_bytes(): per-slab
+                                    complement totals of the exit rows */
+  size_t workspace_bytes;
 } SgTreeSampleArgs;
 
 /* Row statistics of all packed rows followed by the per-request walk. */
 int sg_tree_sample(const SgTreeSampleArgs* args, sg_stream_t stream);
+
+/* Scratch bytes sg_tree_sample needs for num_requests requests over vocab
+ * (4 bytes per 2048-token slab per request).  No reference counterpart. */
+int64_t sg_tree_sample_workspace_bytes(int32_t num_requests, int32_t vocab);
 
 /* Row statistics only (max and sum of exp of each logits row). */
 int sg_row_stats(const float* logits_dev, int64_t row_stride, int32_t vocab,

@@ -67,13 +67,14 @@ class SgTreeSampleArgs(ctypes.Structure):
         ("accept_nodes_dev", c_void_p), ("accept_len_dev", c_void_p),
         ("bonus_dev", c_void_p), ("keep_rows_dev", c_void_p),
         ("status_dev", c_void_p),
+        ("workspace_dev", c_void_p), ("workspace_bytes", c_size),
     ]
 
 
 EXPORTED_SYMBOLS = (
     "sg_abi_version", "sg_last_error", "sg_abi_struct_size",
     "sg_tree_attn_plan", "sg_tree_attn_fwd", "sg_kv_commit",
-    "sg_tree_sample", "sg_row_stats", "sg_exp_probe",
+    "sg_tree_sample", "sg_tree_sample_workspace_bytes", "sg_row_stats", "sg_exp_probe",
 )
 
 _lib = None
@@ -110,6 +111,8 @@ def load() -> ctypes.CDLL:
     lib.sg_kv_commit.argtypes = [ctypes.POINTER(SgKvCommitArgs), c_void_p]
     lib.sg_tree_sample.restype = c_i32
     lib.sg_tree_sample.argtypes = [ctypes.POINTER(SgTreeSampleArgs), c_void_p]
+    lib.sg_tree_sample_workspace_bytes.restype = c_i64
+    lib.sg_tree_sample_workspace_bytes.argtypes = [c_i32, c_i32]
     lib.sg_row_stats.restype = c_i32
     lib.sg_row_stats.argtypes = [c_void_p, c_i64, c_i32, c_i32, c_void_p, c_void_p, c_void_p]
     lib.sg_exp_probe.restype = c_i32

@@ -128,31 +128,73 @@ __device__ __forceinline__ void load_slab(const float* __restrict__ x, int vocab
   }
 }
 
-template <bool kVec4>
-__device__ MZ wave_row_stats(const float* __restrict__ x, int vocab, int lane) {
-  const int slabs = (vocab + kSlab - 1) / kSlab;
-  MZ acc = {-__builtin_inff(), 0.0f};
-  for (int s = 0; s < slabs; ++s) {
-    float v[32];
-    load_slab<kVec4>(x, vocab, s, lane, v);
-    float m = v[0];
+// (m, Z) of slab s from its 32 values per lane (identical in every lane).
+__device__ __forceinline__ MZ slab_stats(const float v[32]) {
+  float m = v[0];
 #pragma unroll
-    for (int k = 1; k < 32; ++k) m = fmaxf(m, v[k]);
-    m = wave_max(m);
-    MZ slab = {m, 0.0f};
-    if (m != -__builtin_inff()) {
-      float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+  for (int k = 1; k < 32; ++k) m = fmaxf(m, v[k]);
+  m = wave_max(m);
+  MZ slab = {m, 0.0f};
+  if (m != -__builtin_inff()) {
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
 #pragma unroll
-      for (int j = 0; j < kLinesPerSlab; ++j) {
-        a0 = a0 + sg_exp(v[4 * j + 0] - m);
-        a1 = a1 + sg_exp(v[4 * j + 1] - m);
-        a2 = a2 + sg_exp(v[4 * j + 2] - m);
-        a3 = a3 + sg_exp(v[4 * j + 3] - m);
-      }
-      slab.z = wave_butterfly_sum((a0 + a1) + (a2 + a3));
+    for (int j = 0; j < kLinesPerSlab; ++j) {
+      a0 = a0 + sg_exp(v[4 * j + 0] - m);
+      a1 = a1 + sg_exp(v[4 * j + 1] - m);
+      a2 = a2 + sg_exp(v[4 * j + 2] - m);
+      a3 = a3 + sg_exp(v[4 * j + 3] - m);
     }
-    const MZ merged = merge_mz(acc, slab);
-    if (lane == (s & (kWave - 1))) acc = merged;
+    slab.z = wave_butterfly_sum((a0 + a1) + (a2 + a3));
+  }
+  return slab;
+}
+
+// One row per workgroup: its four waves compute the statistics of slabs
+// s = wave, wave + 4, ... (the next slab's loads are issued before the
+// current slab's arithmetic), then wave 0 merges the slabs in the canonical
+// order -- slab s into lane s % 64 in increasing s, then the xor butterfly
+// over the lanes -- which makes the result independent of how slabs were
+// spread over waves.
+template <bool kVec4>
+__global__ __launch_bounds__(kStatsThreads) void row_stats_kernel(
+    const float* __restrict__ logits, int64_t row_stride, int vocab, int rows,
+    float* __restrict__ row_max, float* __restrict__ row_sum) {
+  __shared__ float s_m[kMaxSlabs];
+  __shared__ float s_z[kMaxSlabs];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int row = blockIdx.x;
+  if (row >= rows) return;
+  const float* __restrict__ x = logits + row_stride * row;
+  const int slabs = (vocab + kSlab - 1) / kSlab;
+  constexpr int kWavesPerRow = kStatsThreads / kWave;
+  float v[32], w[32];
+  int s = wave;
+  if (s < slabs) load_slab<kVec4>(x, vocab, s, lane, v);
+  while (s < slabs) {
+    const int next = s + kWavesPerRow;
+    if (next < slabs) load_slab<kVec4>(x, vocab, next, lane, w);
+    const MZ a = slab_stats(v);
+    if (lane == 0) {
+      s_m[s] = a.m;
+      s_z[s] = a.z;
+    }
+    if (next >= slabs) break;
+    const int next2 = next + kWavesPerRow;
+    if (next2 < slabs) load_slab<kVec4>(x, vocab, next2, lane, v);
+    const MZ b = slab_stats(w);
+    if (lane == 0) {
+      s_m[next] = b.m;
+      s_z[next] = b.z;
+    }
+    s = next2;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  MZ acc = {-__builtin_inff(), 0.0f};
+  for (int t = lane; t < slabs; t += kWave) {
+    const MZ slab = {s_m[t], s_z[t]};
+    acc = merge_mz(acc, slab);
   }
 #pragma unroll
   for (int d = 32; d >= 1; d >>= 1) {
@@ -161,21 +203,9 @@ __device__ MZ wave_row_stats(const float* __restrict__ x, int vocab, int lane) {
     other.z = __shfl_xor(acc.z, d);
     acc = merge_mz(acc, other);
   }
-  return acc;
-}
-
-// One wavefront per row, four rows per workgroup.
-template <bool kVec4>
-__global__ __launch_bounds__(kStatsThreads) void row_stats_kernel(
-    const float* __restrict__ logits, int64_t row_stride, int vocab, int rows,
-    float* __restrict__ row_max, float* __restrict__ row_sum) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int row = blockIdx.x * (kStatsThreads / kWave) + (threadIdx.x / kWave);
-  if (row >= rows) return;
-  const MZ r = wave_row_stats<kVec4>(logits + row_stride * row, vocab, lane);
   if (lane == 0) {
-    row_max[row] = r.m;
-    row_sum[row] = r.z;
+    row_max[row] = acc.m;
+    row_sum[row] = acc.z;
   }
 }
 
@@ -224,135 +254,224 @@ __device__ __forceinline__ void line_scans(const float e[32], int lane,
   }
 }
 
+// Tree data of one request in LDS and the routing walk over it.
+struct RouteShared {
+  int parent[kMaxTreeRows];
+  int token[kMaxTreeRows];
+  float xchild[kMaxTreeRows];  // x_parent(c)[token(c)] of node c
+  float rm[kMaxTreeRows];
+  float rz[kMaxTreeRows];
+  float u[2 * kMaxTreeRows + 2];
+  int child_tok[kMaxTreeRows];  // children of the exit node, ascending node order
+  int child_count;
+  int exit_node;
+  int depth;
+  int broken;
+};
+
+// Gathers everything the routing reads in one parallel round (the tree, the
+// row statistics, the uniforms and each node's token logit in its parent's
+// row -- the only logits routing touches), then walks on one thread: from v,
+// the children in ascending node order accumulate S += E(x_v[token] - m_v) and
+// the first child with u[2d] * Z_v < S is accepted.  Accepted nodes are
+// written to nodes_out when write_nodes.  Ends with a barrier.
+__device__ void route_request(const SgTreeSampleArgs& a, int req, int r0, int n,
+                              RouteShared& sh, bool write_nodes) {
+  const int tid = threadIdx.x;
+  const float* __restrict__ u = a.uniforms_dev + static_cast<int64_t>(a.uniform_stride) * req;
+  const int n_u = min(a.uniform_stride, 2 * kMaxTreeRows + 2);
+  for (int k = tid; k < n; k += blockDim.x) {
+    const int p = a.parent_dev[r0 + k];
+    const int tok = a.token_dev[r0 + k];
+    sh.parent[k] = p;
+    sh.token[k] = tok;
+    sh.rm[k] = a.row_max_dev[r0 + k];
+    sh.rz[k] = a.row_sum_dev[r0 + k];
+    const bool readable = k > 0 && p >= 0 && p < k && tok >= 0 && tok < a.vocab;
+    sh.xchild[k] = readable ? a.logits_dev[a.logits_row_stride * (r0 + p) + tok] : 0.0f;
+  }
+  for (int k = tid; k < n_u; k += blockDim.x) sh.u[k] = u[k];
+  __syncthreads();
+  if (tid == 0) {
+    int32_t* nodes_out = a.accept_nodes_dev + static_cast<int64_t>(a.max_depth) * req;
+    int v = 0;
+    int depth = 0;
+    int broken = 0;
+    for (;;) {
+      if (2 * depth + 1 >= a.uniform_stride || 2 * depth + 1 >= n_u) {
+        broken = 1;
+        break;
+      }
+      const float m = sh.rm[v];
+      const float threshold = sh.u[2 * depth] * sh.rz[v];
+      float cumulative = 0.0f;
+      int accepted = -1;
+      for (int c = v + 1; c < n; ++c) {
+        if (sh.parent[c] != v) continue;
+        const int tok = sh.token[c];
+        if (tok < 0 || tok >= a.vocab) {
+          accepted = -2;  // draft token outside the vocabulary
+          break;
+        }
+        cumulative = cumulative + sg_exp(sh.xchild[c] - m);
+        if (threshold < cumulative) {
+          accepted = c;
+          break;
+        }
+      }
+      if (accepted >= 0 && depth >= a.max_depth) accepted = -2;
+      if (accepted == -2) {
+        broken = 1;
+        break;
+      }
+      if (accepted < 0) break;
+      if (write_nodes) nodes_out[depth] = accepted;
+      v = accepted;
+      ++depth;
+    }
+    int count = 0;
+    for (int c = v + 1; c < n; ++c)
+      if (sh.parent[c] == v) sh.child_tok[count++] = sh.token[c];
+    sh.child_count = count;
+    sh.exit_node = v;
+    sh.depth = depth;
+    sh.broken = broken;
+  }
+  __syncthreads();
+}
+
+// Walk, part 1.  Grid (request, chunk of kWalkWaves slabs); every workgroup
+// routes its request (cheap, LDS only), workgroup chunk 0 writes the accepted
+// nodes, accept length and keep rows, and every wave computes the complement
+// total of one slab of the exit row:
+//   e = E(x - m) for non-child tokens below vocab, 0 otherwise; group sums
+//   ((e0+e1)+e2)+e3; inclusive Kogge-Stone scan over the 64 lanes of a line;
+//   slab total = sequential sum of the line totals.
 template <bool kVec4>
-__global__ __launch_bounds__(kWalkThreads) void tree_walk_kernel(SgTreeSampleArgs a) {
-  __shared__ int s_child_node[kMaxTreeRows];
+__global__ __launch_bounds__(kWalkThreads) void exit_totals_kernel(SgTreeSampleArgs a) {
+  __shared__ RouteShared sh;
+  const int req = blockIdx.x;
+  const int chunk = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int r0 = a.row_offset_dev[req];
+  const int n = a.row_offset_dev[req + 1] - r0;
+  if (n < 1 || n > kMaxTreeRows) {
+    if (chunk == 0 && tid == 0) {
+      a.accept_len_dev[req] = -1;
+      a.bonus_dev[req] = -1;
+      if (a.status_dev) atomicExch(a.status_dev, SG_EINVAL);
+    }
+    return;
+  }
+  int32_t* nodes_out = a.accept_nodes_dev + static_cast<int64_t>(a.max_depth) * req;
+  if (chunk == 0)
+    for (int k = tid; k < a.max_depth; k += blockDim.x) nodes_out[k] = -1;
+  __syncthreads();
+  route_request(a, req, r0, n, sh, chunk == 0);
+  if (chunk == 0) {
+    if (tid == 0) {
+      a.accept_len_dev[req] = sh.broken ? -1 : sh.depth;
+      if (sh.broken) {
+        a.bonus_dev[req] = -1;
+        if (a.status_dev) atomicExch(a.status_dev, SG_EINVAL);
+      }
+    }
+    if (a.keep_rows_dev) {
+      __syncthreads();  // nodes_out written by thread 0
+      int32_t* keep = a.keep_rows_dev + static_cast<int64_t>(a.max_depth + 1) * req;
+      for (int k = tid; k <= a.max_depth; k += blockDim.x)
+        keep[k] = (k == 0) ? 0 : (!sh.broken && k <= sh.depth ? nodes_out[k - 1] : -1);
+    }
+  }
+  if (sh.broken) return;
+  const int slabs = (a.vocab + kSlab - 1) / kSlab;
+  const int s = chunk * kWalkWaves + wave;
+  if (s >= slabs) return;
+  const int64_t row = r0 + sh.exit_node;
+  const float* __restrict__ x = a.logits_dev + a.logits_row_stride * row;
+  const float m = sh.rm[sh.exit_node];
+  float e[32], incl[kLinesPerSlab], total[kLinesPerSlab];
+  exit_values<kVec4>(x, a.vocab, m, s, lane, child_bits(sh.child_tok, sh.child_count, s, lane),
+                     e);
+  line_scans(e, lane, incl, total);
+  float lp = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kLinesPerSlab; ++j) lp = lp + total[j];
+  if (lane == 0)
+    static_cast<float*>(a.workspace_dev)[static_cast<int64_t>(req) * slabs + s] = lp;
+}
+
+// Walk, part 2 (one workgroup per request): slab prefixes P_s (sequential),
+// C = P_slabs, threshold u[2d+1] * C; the bonus is the first non-child token
+// whose running value (P_s + line prefix + lane prefix + its group's
+// elements) exceeds the threshold; fallback: the largest non-child token.
+// A slab whose P_s + T_s lies below threshold - 1e-4 * C cannot hold that
+// token (its running values differ from P_s + T_s by a few roundings), so
+// the ordered scan starts at the first slab that may.
+template <bool kVec4>
+__global__ __launch_bounds__(kWalkThreads) void exit_find_kernel(SgTreeSampleArgs a) {
   __shared__ int s_child_tok[kMaxTreeRows];
   __shared__ int s_wave_count[kWalkWaves];
-  __shared__ float s_slab_total[kMaxSlabs];
   __shared__ float s_slab_prefix[kMaxSlabs + 1];
-  __shared__ int s_child_count;
-  __shared__ int s_accepted;
+  __shared__ int s_first;
   __shared__ int s_candidate;
   __shared__ float s_threshold;
-
   const int req = blockIdx.x;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
   const int r0 = a.row_offset_dev[req];
   const int n = a.row_offset_dev[req + 1] - r0;
-  const float* __restrict__ u = a.uniforms_dev + static_cast<int64_t>(a.uniform_stride) * req;
-  int32_t* nodes_out = a.accept_nodes_dev + static_cast<int64_t>(a.max_depth) * req;
-  if (n < 1 || n > kMaxTreeRows) {
-    if (tid == 0) {
-      a.accept_len_dev[req] = -1;
-      a.bonus_dev[req] = -1;
-      if (a.status_dev) atomicExch(a.status_dev, SG_EINVAL);
-    }
-    return;
-  }
-  for (int k = tid; k < a.max_depth; k += kWalkThreads) nodes_out[k] = -1;
-
-  int v = 0;
-  int depth = 0;
-  bool broken = false;
-  for (;;) {
-    __syncthreads();
-    // Children of v in ascending node order.
-    const bool is_child = tid < n && tid > v && a.parent_dev[r0 + tid] == v;
-    const uint64_t mask = __ballot(is_child);
-    if (lane == 0) s_wave_count[wave] = __popcll(mask);
-    __syncthreads();
-    int offset = 0;
-    int total = 0;
-    for (int w = 0; w < kWalkWaves; ++w) {
-      offset += (w < wave) ? s_wave_count[w] : 0;
-      total += s_wave_count[w];
-    }
-    if (is_child) {
-      const int pos = offset + __popcll(mask & ((1ull << lane) - 1ull));
-      s_child_node[pos] = tid;
-      s_child_tok[pos] = a.token_dev[r0 + tid];
-    }
-    if (tid == 0) s_child_count = total;
-    __syncthreads();
-    if (tid == 0) {
-      int accepted = -1;
-      if (2 * depth + 1 >= a.uniform_stride) {
-        accepted = -2;
-      } else {
-        const int64_t row = r0 + v;
-        const float* __restrict__ x = a.logits_dev + a.logits_row_stride * row;
-        const float m = a.row_max_dev[row];
-        const float threshold = u[2 * depth] * a.row_sum_dev[row];
-        float cumulative = 0.0f;
-        for (int k = 0; k < s_child_count; ++k) {
-          const int tok = s_child_tok[k];
-          if (tok < 0 || tok >= a.vocab) {
-            accepted = -2;  // draft token outside the vocabulary
-            break;
-          }
-          cumulative = cumulative + sg_exp(x[tok] - m);
-          if (threshold < cumulative) {
-            accepted = s_child_node[k];
-            break;
-          }
-        }
-        if (accepted >= 0 && depth >= a.max_depth) accepted = -2;
-      }
-      s_accepted = accepted;
-    }
-    __syncthreads();
-    const int accepted = s_accepted;
-    if (accepted == -2) {
-      broken = true;
-      break;
-    }
-    if (accepted < 0) break;
-    if (tid == 0) nodes_out[depth] = accepted;
-    v = accepted;
-    ++depth;
-  }
-  if (broken) {
-    if (tid == 0) {
-      a.accept_len_dev[req] = -1;
-      a.bonus_dev[req] = -1;
-      if (a.status_dev) atomicExch(a.status_dev, SG_EINVAL);
-    }
-    return;
-  }
-
-  // Exit at v: draw the bonus from the complement of v's children.
-  const int64_t row = r0 + v;
-  const float* __restrict__ x = a.logits_dev + a.logits_row_stride * row;
-  const float m = a.row_max_dev[row];
-  const int count = s_child_count;
-  const int slabs = (a.vocab + kSlab - 1) / kSlab;
-
-  for (int s = wave; s < slabs; s += kWalkWaves) {
-    float e[32], incl[kLinesPerSlab], total[kLinesPerSlab];
-    exit_values<kVec4>(x, a.vocab, m, s, lane, child_bits(s_child_tok, count, s, lane), e);
-    line_scans(e, lane, incl, total);
-    float lp = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kLinesPerSlab; ++j) lp = lp + total[j];
-    if (lane == 0) s_slab_total[s] = lp;
-  }
+  if (n < 1 || n > kMaxTreeRows) return;
+  const int depth = a.accept_len_dev[req];
+  if (depth < 0) return;  // broken walk, reported by part 1
+  const int v = depth > 0 ? a.accept_nodes_dev[static_cast<int64_t>(a.max_depth) * req + depth - 1]
+                          : 0;
+  // Children of the exit node in ascending node order.
+  const bool is_child = tid < n && tid > v && a.parent_dev[r0 + tid] == v;
+  const uint64_t mask = __ballot(is_child);
+  if (lane == 0) s_wave_count[wave] = __popcll(mask);
   __syncthreads();
+  int offset = 0;
+  int count = 0;
+  for (int w = 0; w < kWalkWaves; ++w) {
+    offset += (w < wave) ? s_wave_count[w] : 0;
+    count += s_wave_count[w];
+  }
+  if (is_child) s_child_tok[offset + __popcll(mask & ((1ull << lane) - 1ull))] =
+      a.token_dev[r0 + tid];
+  const int slabs = (a.vocab + kSlab - 1) / kSlab;
+  const float* __restrict__ totals =
+      static_cast<const float*>(a.workspace_dev) + static_cast<int64_t>(req) * slabs;
+  const float* __restrict__ u = a.uniforms_dev + static_cast<int64_t>(a.uniform_stride) * req;
   if (tid == 0) {
     float prefix = 0.0f;
     for (int s = 0; s < slabs; ++s) {
       s_slab_prefix[s] = prefix;
-      prefix = prefix + s_slab_total[s];
+      prefix = prefix + totals[s];
     }
     s_slab_prefix[slabs] = prefix;
-    s_threshold = u[2 * depth + 1] * prefix;
+    const float threshold = u[2 * depth + 1] * prefix;
+    const float bound = threshold - 1e-4f * prefix;
+    int first = slabs;
+    for (int s = 0; s < slabs; ++s) {
+      if (s_slab_prefix[s] + totals[s] > bound) {
+        first = s;
+        break;
+      }
+    }
+    s_first = first;
+    s_threshold = threshold;
     s_candidate = INT_MAX;
   }
   __syncthreads();
+  const int64_t row = r0 + v;
+  const float* __restrict__ x = a.logits_dev + a.logits_row_stride * row;
+  const float m = a.row_max_dev[row];
   const float threshold = s_threshold;
-  for (int base = 0; base < slabs; base += kWalkWaves) {
+  for (int base = s_first; base < slabs; base += kWalkWaves) {
     const int s = base + wave;
     if (s < slabs) {
       float e[32], incl[kLinesPerSlab], total[kLinesPerSlab];
@@ -398,13 +517,7 @@ __global__ __launch_bounds__(kWalkThreads) void tree_walk_kernel(SgTreeSampleArg
         }
       }
     }
-    a.accept_len_dev[req] = depth;
     a.bonus_dev[req] = bonus;
-  }
-  if (a.keep_rows_dev) {
-    int32_t* keep = a.keep_rows_dev + static_cast<int64_t>(a.max_depth + 1) * req;
-    for (int k = tid; k <= a.max_depth; k += kWalkThreads)
-      keep[k] = (k == 0) ? 0 : (k <= depth ? nodes_out[k - 1] : -1);
   }
 }
 
@@ -421,8 +534,7 @@ bool vec4_ok(const float* p, int64_t stride, int vocab) {
 int launch_row_stats(const float* logits, int64_t stride, int vocab, int rows,
                      float* row_max, float* row_sum, hipStream_t stream) {
   if (rows == 0) return SG_OK;
-  const int rows_per_block = kStatsThreads / kWave;
-  const dim3 grid((rows + rows_per_block - 1) / rows_per_block);
+  const dim3 grid(rows);  // one workgroup per row
   if (vec4_ok(logits, stride, vocab)) {
     hipLaunchKernelGGL(row_stats_kernel<true>, grid, dim3(kStatsThreads), 0, stream,
                        logits, stride, vocab, rows, row_max, row_sum);
@@ -451,6 +563,13 @@ extern "C" int sg_row_stats(const float* logits_dev, int64_t row_stride, int32_t
                           row_sum_dev, reinterpret_cast<hipStream_t>(stream));
 }
 
+extern "C" int64_t sg_tree_sample_workspace_bytes(int32_t num_requests, int32_t vocab) {
+  using namespace sg;
+  if (num_requests < 0 || vocab < 1) return 0;
+  return static_cast<int64_t>(num_requests) * ((vocab + kSlab - 1) / kSlab) *
+         static_cast<int64_t>(sizeof(float));
+}
+
 extern "C" int sg_tree_sample(const SgTreeSampleArgs* args, sg_stream_t stream) {
   using namespace sg;
   clear_error();
@@ -467,16 +586,25 @@ extern "C" int sg_tree_sample(const SgTreeSampleArgs* args, sg_stream_t stream) 
                  a.uniforms_dev && a.row_max_dev && a.row_sum_dev && a.accept_len_dev &&
                  a.bonus_dev && (a.max_depth == 0 || a.accept_nodes_dev),
              "null device pointer");
+  SG_REQUIRE(a.workspace_dev != nullptr &&
+                 a.workspace_bytes >= sg_tree_sample_workspace_bytes(a.num_requests, a.vocab),
+             "workspace below sg_tree_sample_workspace_bytes");
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   int rc = launch_row_stats(a.logits_dev, a.logits_row_stride, a.vocab, a.num_rows,
                             a.row_max_dev, a.row_sum_dev, s);
   if (rc != SG_OK) return rc;
+  const int slabs = (a.vocab + kSlab - 1) / kSlab;
+  const dim3 grid1(a.num_requests, (slabs + kWalkWaves - 1) / kWalkWaves);
   if (vec4_ok(a.logits_dev, a.logits_row_stride, a.vocab)) {
-    hipLaunchKernelGGL(tree_walk_kernel<true>, dim3(a.num_requests), dim3(kWalkThreads), 0,
-                       s, a);
+    hipLaunchKernelGGL(exit_totals_kernel<true>, grid1, dim3(kWalkThreads), 0, s, a);
+    SG_LAUNCH_CHECK();
+    hipLaunchKernelGGL(exit_find_kernel<true>, dim3(a.num_requests), dim3(kWalkThreads), 0, s,
+                       a);
   } else {
-    hipLaunchKernelGGL(tree_walk_kernel<false>, dim3(a.num_requests), dim3(kWalkThreads), 0,
-                       s, a);
+    hipLaunchKernelGGL(exit_totals_kernel<false>, grid1, dim3(kWalkThreads), 0, s, a);
+    SG_LAUNCH_CHECK();
+    hipLaunchKernelGGL(exit_find_kernel<false>, dim3(a.num_requests), dim3(kWalkThreads), 0, s,
+                       a);
   }
   SG_LAUNCH_CHECK();
   return SG_OK;

@@ -265,6 +265,7 @@ class SampleResult:
     row_max: torch.Tensor       # [R] f32
     row_sum: torch.Tensor       # [R] f32
     status: torch.Tensor        # [1] i32
+    workspace: torch.Tensor | None = None  # per-slab complement totals of the exit rows
 
 
 def tree_sample(logits: torch.Tensor, row_offset: torch.Tensor, parent: torch.Tensor,
@@ -300,6 +301,9 @@ def tree_sample(logits: torch.Tensor, row_offset: torch.Tensor, parent: torch.Te
             row_sum=torch.empty(rows, dtype=torch.float32, device=dev),
             status=torch.zeros(1, dtype=torch.int32, device=dev),
         )
+    ws_bytes = int(_lib.load().sg_tree_sample_workspace_bytes(n, logits.shape[1]))
+    if out.workspace is None or out.workspace.numel() < ws_bytes:
+        out.workspace = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
     a = _lib.SgTreeSampleArgs()
     a.num_requests = n
     a.num_rows = rows
@@ -319,6 +323,8 @@ def tree_sample(logits: torch.Tensor, row_offset: torch.Tensor, parent: torch.Te
     a.bonus_dev = out.bonus.data_ptr()
     a.keep_rows_dev = out.keep_rows.data_ptr()
     a.status_dev = out.status.data_ptr()
+    a.workspace_dev = out.workspace.data_ptr()
+    a.workspace_bytes = out.workspace.numel()
     _lib.check(_lib.load().sg_tree_sample(ctypes.byref(a), _stream_handle()), "sg_tree_sample")
     return out
 

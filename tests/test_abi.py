@@ -19,7 +19,7 @@ def _declared_functions():
 
 def test_library_loads_and_struct_sizes_match():
     lib = _lib.load()
-    assert lib.sg_abi_version() == 1
+    assert lib.sg_abi_version() == 2
 
 
 def test_every_declared_symbol_is_exported():
