@@ -64,9 +64,30 @@ __device__ __forceinline__ float sg_exp(float x) {
   p = __builtin_fmaf(p, r, 0.5f);
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
-  const int bits = (static_cast<int>(n) + 127) << 23;
-  float y = p * __int_as_float(bits);
+  // p * 2^n, exact scale (n in [-126, 127]); ldexp rounds a subnormal result
+  // exactly as the multiplication by the normal power of two would.
+  float y = __builtin_ldexpf(p, static_cast<int>(n));
   y = (x > 88.0f) ? __builtin_inff() : y;
+  return live ? y : 0.0f;
+}
+
+// E(x) for x <= 0 (every argument of the form value - max): the same
+// operations as sg_exp without the upper clamp and overflow select, which
+// cannot apply there, so the results are identical.
+__device__ __forceinline__ float sg_exp_nonpos(float x) {
+  const bool live = x >= -87.0f;
+  const float xc = fmaxf(x, -87.0f);
+  const float n = __builtin_rintf(xc * SG_LOG2E);
+  float r = __builtin_fmaf(-n, SG_LN2_HI, xc);
+  r = __builtin_fmaf(-n, SG_LN2_LO, r);
+  float p = SG_C6;
+  p = __builtin_fmaf(p, r, SG_C5);
+  p = __builtin_fmaf(p, r, SG_C4);
+  p = __builtin_fmaf(p, r, SG_C3);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  const float y = __builtin_ldexpf(p, static_cast<int>(n));
   return live ? y : 0.0f;
 }
 
@@ -102,7 +123,16 @@ template <bool kVec4>
 __device__ __forceinline__ void load_slab(const float* __restrict__ x, int vocab,
                                           int slab, int lane, float v[32]) {
   const int base = slab * kSlab + 4 * lane;
-  if (kVec4) {
+  if (kVec4 && (slab + 1) * kSlab <= vocab) {  // full slab: no bounds checks
+#pragma unroll
+    for (int j = 0; j < kLinesPerSlab; ++j) {
+      const float4 q = *reinterpret_cast<const float4*>(x + base + kLine * j);
+      v[4 * j + 0] = q.x;
+      v[4 * j + 1] = q.y;
+      v[4 * j + 2] = q.z;
+      v[4 * j + 3] = q.w;
+    }
+  } else if (kVec4) {
 #pragma unroll
     for (int j = 0; j < kLinesPerSlab; ++j) {
       const int t = base + kLine * j;
@@ -139,10 +169,10 @@ __device__ __forceinline__ MZ slab_stats(const float v[32]) {
     float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
 #pragma unroll
     for (int j = 0; j < kLinesPerSlab; ++j) {
-      a0 = a0 + sg_exp(v[4 * j + 0] - m);
-      a1 = a1 + sg_exp(v[4 * j + 1] - m);
-      a2 = a2 + sg_exp(v[4 * j + 2] - m);
-      a3 = a3 + sg_exp(v[4 * j + 3] - m);
+      a0 = a0 + sg_exp_nonpos(v[4 * j + 0] - m);
+      a1 = a1 + sg_exp_nonpos(v[4 * j + 1] - m);
+      a2 = a2 + sg_exp_nonpos(v[4 * j + 2] - m);
+      a3 = a3 + sg_exp_nonpos(v[4 * j + 3] - m);
     }
     slab.z = wave_butterfly_sum((a0 + a1) + (a2 + a3));
   }
@@ -231,7 +261,7 @@ __device__ __forceinline__ void exit_values(const float* __restrict__ x, int voc
   load_slab<kVec4>(x, vocab, slab, lane, e);
 #pragma unroll
   for (int k = 0; k < 32; ++k) {
-    const float val = sg_exp(e[k] - m);
+    const float val = sg_exp_nonpos(e[k] - m);
     e[k] = ((bits >> k) & 1u) ? 0.0f : val;
   }
 }
@@ -263,6 +293,8 @@ struct RouteShared {
   float rz[kMaxTreeRows];
   float u[2 * kMaxTreeRows + 2];
   int child_tok[kMaxTreeRows];  // children of the exit node, ascending node order
+  int first_child[kMaxTreeRows];   // smallest child of node v, -1 for a leaf
+  int next_sibling[kMaxTreeRows];  // next larger node with the same parent, -1 if none
   int child_count;
   int exit_node;
   int depth;
@@ -292,6 +324,25 @@ __device__ void route_request(const SgTreeSampleArgs& a, int req, int r0, int n,
   }
   for (int k = tid; k < n_u; k += blockDim.x) sh.u[k] = u[k];
   __syncthreads();
+  // Children in ascending node order as first-child / next-sibling links.
+  for (int k = tid; k < n; k += blockDim.x) {
+    int first = -1;
+    for (int c = k + 1; c < n; ++c)
+      if (sh.parent[c] == k) {
+        first = c;
+        break;
+      }
+    sh.first_child[k] = first;
+    int next = -1;
+    const int p = sh.parent[k];
+    for (int c = k + 1; k > 0 && c < n; ++c)
+      if (sh.parent[c] == p) {
+        next = c;
+        break;
+      }
+    sh.next_sibling[k] = next;
+  }
+  __syncthreads();
   if (tid == 0) {
     int32_t* nodes_out = a.accept_nodes_dev + static_cast<int64_t>(a.max_depth) * req;
     int v = 0;
@@ -306,8 +357,7 @@ __device__ void route_request(const SgTreeSampleArgs& a, int req, int r0, int n,
       const float threshold = sh.u[2 * depth] * sh.rz[v];
       float cumulative = 0.0f;
       int accepted = -1;
-      for (int c = v + 1; c < n; ++c) {
-        if (sh.parent[c] != v) continue;
+      for (int c = sh.first_child[v]; c >= 0; c = sh.next_sibling[c]) {
         const int tok = sh.token[c];
         if (tok < 0 || tok >= a.vocab) {
           accepted = -2;  // draft token outside the vocabulary
@@ -330,8 +380,8 @@ __device__ void route_request(const SgTreeSampleArgs& a, int req, int r0, int n,
       ++depth;
     }
     int count = 0;
-    for (int c = v + 1; c < n; ++c)
-      if (sh.parent[c] == v) sh.child_tok[count++] = sh.token[c];
+    for (int c = sh.first_child[v]; c >= 0; c = sh.next_sibling[c])
+      sh.child_tok[count++] = sh.token[c];
     sh.child_count = count;
     sh.exit_node = v;
     sh.depth = depth;
@@ -415,6 +465,7 @@ __global__ __launch_bounds__(kWalkThreads) void exit_find_kernel(SgTreeSampleArg
   __shared__ int s_child_tok[kMaxTreeRows];
   __shared__ int s_wave_count[kWalkWaves];
   __shared__ float s_slab_prefix[kMaxSlabs + 1];
+  __shared__ float s_total[kMaxSlabs];
   __shared__ int s_first;
   __shared__ int s_candidate;
   __shared__ float s_threshold;
@@ -446,18 +497,20 @@ __global__ __launch_bounds__(kWalkThreads) void exit_find_kernel(SgTreeSampleArg
   const float* __restrict__ totals =
       static_cast<const float*>(a.workspace_dev) + static_cast<int64_t>(req) * slabs;
   const float* __restrict__ u = a.uniforms_dev + static_cast<int64_t>(a.uniform_stride) * req;
+  for (int s = tid; s < slabs; s += blockDim.x) s_total[s] = totals[s];
+  __syncthreads();
   if (tid == 0) {
     float prefix = 0.0f;
     for (int s = 0; s < slabs; ++s) {
       s_slab_prefix[s] = prefix;
-      prefix = prefix + totals[s];
+      prefix = prefix + s_total[s];
     }
     s_slab_prefix[slabs] = prefix;
     const float threshold = u[2 * depth + 1] * prefix;
     const float bound = threshold - 1e-4f * prefix;
     int first = slabs;
     for (int s = 0; s < slabs; ++s) {
-      if (s_slab_prefix[s] + totals[s] > bound) {
+      if (s_slab_prefix[s] + s_total[s] > bound) {
         first = s;
         break;
       }
