@@ -47,11 +47,13 @@ typedef __attribute__((ext_vector_type(4))) short short4_t;
 typedef __attribute__((ext_vector_type(8))) short short8_t;
 typedef __attribute__((address_space(3))) short4_t lds_short4;
 
-constexpr int kThreads = 512;
+constexpr int kThreads = 256;
 constexpr int kQPerUnit = 128;
-constexpr int kTileKeys = 64;
+constexpr int kTileKeys = 32;
+constexpr int kBlocksPerTile = kTileKeys / 32;  // 32-key MFMA blocks per tile
+constexpr int kListsPerCU = 2;                  // resident workgroups per CU
 constexpr int kStages = 4;
-constexpr int kWaves = 8;
+constexpr int kWaves = 4;
 constexpr int kMaxTreeRows = 256;
 constexpr int kAncWords = kMaxTreeRows / 32;
 constexpr int kMergeThreads = 256;
@@ -197,7 +199,7 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
   static_assert(DMAS >= 1, "tile too small for the workgroup");
   static_assert(kStages == 4, "the issue schedule assumes a 4-tile ring");
   static_assert(kStages * STAGEB <= 65536, "ring offsets must fit the LDS immediate");
-  static_assert(2 * kStages * STAGEB >= 6 * STATE * 64 * 4, "merge scratch");
+  static_assert(2 * ((kStages * STAGEB) / (STATE * 64 * 4)) >= 2, "merge scratch");
   // Rings of kStages tiles of K and of V; reused as the merge scratch at the end.
   __shared__ __align__(1024) unsigned char s_k[kStages * STAGEB];
   __shared__ __align__(1024) unsigned char s_v[kStages * STAGEB];
@@ -216,13 +218,13 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
   // two blocks of one tile).  Every wave handles one 32-key block per
   // iteration.  Waves beyond nq*streams repeat stream 0's work on the same
   // LDS data and discard it.
-  const int streams = nq <= 2 ? 4 : 2;
-  const int per_iter = streams / 2;             // tiles consumed per iteration
+  const int streams = nq <= 2 ? 2 : 1;
+  const int per_iter = streams / kBlocksPerTile;  // tiles consumed per iteration
   const int qg = wave % nq;
   const int ks = wave / nq;                     // key stream of this wave
   const bool active = ks < streams;
-  const int my_tile = active ? (ks >> 1) : 0;   // tile of the iteration this wave takes
-  const int my_blk = active ? (ks & 1) : 0;     // 32-key block inside that tile
+  const int my_tile = active ? ks / kBlocksPerTile : 0;  // tile of the window this wave takes
+  const int my_blk = active ? ks % kBlocksPerTile : 0;   // 32-key block inside that tile
   const int m = qg * 32 + col;                  // query vector inside the unit
   const int r_local = m / G;                    // query row inside the tile
   const int head = u.kv_head * G + (m - r_local * G);
@@ -339,10 +341,10 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
   //     ring keeps 2.5 tiles in flight.
   //   per_iter 2: lk 2, lv 1, no lag; one group (two tiles) in flight.
   const int groups = (tiles + per_iter - 1) / per_iter;
-  const bool pingpong = per_iter == 1;
+  const bool pingpong = false;
   const bool lag = pingpong && ks == 1;
   const int lk = kStages / per_iter;
-  const int lv = pingpong ? 2 : 1;
+  const int lv = pingpong ? 2 : lk - 1;
   auto group_tiles = [&](int grp) {
     return grp < 0 ? 0 : max(0, min(per_iter, tiles - grp * per_iter));
   };
@@ -360,7 +362,8 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
       case 2: __builtin_amdgcn_s_waitcnt(vmcnt_encoding(2 * DMAS)); break;
       case 3: __builtin_amdgcn_s_waitcnt(vmcnt_encoding(3 * DMAS)); break;
       case 4: __builtin_amdgcn_s_waitcnt(vmcnt_encoding(4 * DMAS)); break;
-      default: __builtin_amdgcn_s_waitcnt(vmcnt_encoding(5 * DMAS)); break;
+      case 5: __builtin_amdgcn_s_waitcnt(vmcnt_encoding(5 * DMAS)); break;
+      default: __builtin_amdgcn_s_waitcnt(vmcnt_encoding(6 * DMAS)); break;
     }
   };
   // Window i needs V(i) (issued first in window i-lv) and K(i+1) (issued last
@@ -368,7 +371,11 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
   // i-2 and all of window i-1 may still be in flight.  per_iter 2: both come
   // from window i-1, the latest window, so nothing may be in flight.
   auto newer_before = [&](int i) {
-    if (!pingpong) return 0;
+    if (!pingpong) {
+      int c = 0;
+      for (int j = i + 2 - lk; j < i; ++j) c += group_tiles(j + lv) + group_tiles(j + lk);
+      return c;
+    }
     return group_tiles(i + 2) + group_tiles(i + 1) + group_tiles(i + 3);
   };
 
@@ -487,7 +494,9 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
     wait_halves(group_tiles(0) + group_tiles(1) + group_tiles(1) + group_tiles(2) +
                 group_tiles(3));
   } else {
-    wait_halves(group_tiles(0) + group_tiles(1));
+    int newer = 0;
+    for (int j = 1 - lk; j < 0; ++j) newer += group_tiles(j + lv) + group_tiles(j + lk);
+    wait_halves(newer);
   }
   __syncthreads();
   floatx16 s_next;
@@ -499,6 +508,37 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
     wait_halves(newer_before(i));
     __syncthreads();
     issue(i);
+  };
+  // Windows whose issued tiles are all full prefix tiles (i < fast_end) need
+  // none of the schedule arithmetic: the wait count is a constant, the ring
+  // stages are compile-time (K group i+lk lands in group i's stage, V group
+  // i+lk-1 one group earlier) and the sources are one multiply away.
+  const int fast_end = tiles_full / per_iter - lk;
+  const int64_t tile_bytes = static_cast<int64_t>(kTileKeys) * cstride * 2;
+  const uint32_t k_lds_wave = lds_addr(s_k) + wave * DMAS * 1024;
+  const uint32_t v_lds_wave = lds_addr(s_v) + wave * DMAS * 1024;
+  auto fast_window = [&](int i, auto per_tag, auto cur_tag) {
+    constexpr int PER = decltype(per_tag)::value;  // tiles per window
+    constexpr int kCur = decltype(cur_tag)::value;  // ring stage of group i's first tile
+    constexpr int LK = kStages / PER;
+    // per_iter 1: windows i-2 and i-1 each issued one K and one V tile.
+    wait_halves(PER == 1 ? 4 : 0);
+    __syncthreads();
+    const unsigned char* kb = reinterpret_cast<const unsigned char*>(kc) +
+                              static_cast<int64_t>((i + LK) * PER) * tile_bytes;
+    const unsigned char* vb = reinterpret_cast<const unsigned char*>(vc) +
+                              static_cast<int64_t>((i + LK - 1) * PER) * tile_bytes;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+#pragma unroll
+      for (int d = 0; d < DMAS; ++d)
+        dma16(vb + k * tile_bytes, v_dma[d],
+              v_lds_wave + ((kCur + kStages - PER + k) % kStages) * STAGEB + 1024 * d);
+#pragma unroll
+      for (int d = 0; d < DMAS; ++d)
+        dma16(kb + k * tile_bytes, k_dma[d],
+              k_lds_wave + ((kCur + k) % kStages) * STAGEB + 1024 * d);
+    }
   };
   // Softmax of the current block interleaved with the next block's QK MFMAs;
   // leaves the probabilities in pf.
@@ -525,9 +565,13 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
   const int steady_end = max(0, tiles_full / per_iter - 1);
   int i = 0;
   bf16x8 pf[2];
-  if (!pingpong) {
+  if (per_iter == 2) {
     auto step = [&](int w, auto cur_tag, auto next_tag) {
-      window(w);
+      if (w < fast_end) {
+        fast_window(w, IntTag<2>{}, cur_tag);
+      } else {
+        window(w);
+      }
       softmax_qk(decltype(next_tag)::value, pf);
       pv(pf, decltype(cur_tag)::value);
     };
@@ -538,7 +582,11 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
   } else if (!lag) {
     auto step = [&](int w, auto cur_tag) {
       constexpr int kCur = decltype(cur_tag)::value;
-      window(w);
+      if (w < fast_end) {
+        fast_window(w, IntTag<1>{}, cur_tag);
+      } else {
+        window(w);
+      }
       softmax_qk((kCur + 1) % kStages, pf);
       pv(pf, kCur);
     };
@@ -675,7 +723,7 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
 // One workgroup per work list (one per CU): the units of list b are
 // units[bin_offset[b] .. bin_offset[b+1]), processed in order.
 template <int D>
-__global__ __launch_bounds__(kThreads, 1) void tree_attn_kernel(SgTreeAttnArgs a) {
+__global__ __launch_bounds__(kThreads, kListsPerCU) void tree_attn_kernel(SgTreeAttnArgs a) {
   const PlanHeader* hdr = static_cast<const PlanHeader*>(a.plan_dev);
   const AttnUnit* units = reinterpret_cast<const AttnUnit*>(hdr + 1);
   const int32_t* bin_offset = reinterpret_cast<const int32_t*>(
@@ -776,7 +824,7 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
     work += static_cast<int64_t>(num_kv_heads) * tiles *
             ((prefix_len_host[i] + kTileKeys - 1) / kTileKeys + 1);
   }
-  const int64_t target = target_units_hint > 0 ? target_units_hint : kDefaultCUs;
+  const int64_t target = target_units_hint > 0 ? target_units_hint : kDefaultCUs * kListsPerCU;
   int64_t chunk = INT32_MAX;
   if (base_units > 0 && base_units < target) {
     const int64_t per_unit = std::max<int64_t>(4, (work + target - 1) / target);
@@ -842,7 +890,7 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
         (units[k].key_end - units[k].key_begin + kTileKeys - 1) / kTileKeys +
         ((units[k].flags & 1) ? (rows + kTileKeys - 1) / kTileKeys : 0);
     const int nq = (units[k].row_count * G + 31) / 32;
-    cost[k] = nq <= 2 ? 550 + 114 * tiles : 840 + 175 * tiles;
+    cost[k] = nq <= 2 ? 550 + 57 * tiles : 840 + 88 * tiles;
   }
   std::vector<size_t> order(units.size());
   std::iota(order.begin(), order.end(), size_t{0});

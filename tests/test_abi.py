@@ -37,7 +37,7 @@ def _check_plan(wl, target):
     header, units, merges, bins = ops.decode_plan(plan)
     assert header[0] == 0x53475041 and header[2] == plan.merges
     # work lists: one per workgroup, contiguous, covering every unit once
-    assert header[7] == plan.units == min(target if target > 0 else 256, len(units))
+    assert header[7] == plan.units == min(target if target > 0 else 512, len(units))
     assert bins[0] == 0 and bins[-1] == len(units) and (np.diff(bins) >= 1).all()
     rows_per_tile = 128 // (wl.num_q_heads // wl.num_kv_heads)
     cover = {}
@@ -75,9 +75,9 @@ def _check_plan(wl, target):
     assert plan.workspace_bytes == partials * 128 * (wl.head_dim + 2) * 4
     # Balanced lists: no list exceeds the mean load by more than its largest unit.
     def cost(u):
-        tiles = (u[5] - u[4] + 63) // 64 + ((int(wl.rows[u[0]]) + 63) // 64 if u[7] & 1 else 0)
+        tiles = (u[5] - u[4] + 31) // 32 + ((int(wl.rows[u[0]]) + 31) // 32 if u[7] & 1 else 0)
         nq = (u[3] * (wl.num_q_heads // wl.num_kv_heads) + 31) // 32
-        return 550 + 114 * tiles if nq <= 2 else 840 + 175 * tiles
+        return 550 + 57 * tiles if nq <= 2 else 840 + 88 * tiles
     costs = [cost(u) for u in units.tolist()]
     loads = [sum(costs[bins[b]:bins[b + 1]]) for b in range(len(bins) - 1)]
     assert max(loads) <= sum(costs) / len(loads) + max(costs)
