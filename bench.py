@@ -13,6 +13,9 @@ Also reported in the same JSON line:
               rows/s, algorithmic GB/s and the fraction of 8 TB/s (= "roofline");
   commit      per-call time of sg_kv_commit;
   sampler     tree sampling over 64 x 32 nodes, vocab 151936 (nodes/s, GB/s);
+  long_context the heterogeneous long-context wave (128 requests, prefixes
+              log-uniform 8k-32k, 4096 rows): attention, commit, and tree
+              sampling over fp32 logits of every packed row (one input set);
   cpu_baseline the reference's CPU path restated (dense packed mask + SDPA in
               fp32) on a bounded sample, timed on this host's cores.
 """
@@ -43,6 +46,7 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-sampler", action="store_true")
+    p.add_argument("--no-long-context", action="store_true")
     p.add_argument("--cpu-requests", type=int, default=16,
                    help="requests in the CPU baseline's dense packed sample")
     p.add_argument("--target-units", type=int, default=0)
@@ -139,6 +143,92 @@ def sampler_bench(torch, W, ops, device, iters, warmup):
     ms = time_calls(torch, call, iters)
     wl = sets[0]["wl"]
     return wl, ms, sets
+
+
+def long_context_bench(torch, np, W, ops, device, iters=20, warmup=3):
+    """The long-context wave: 128 requests, prefixes log-uniform in 8k-32k,
+    tiers {1,16,32,64,128} under a 4096-row budget, one attention layer, the
+    commit, and tree sampling over fp32 logits [4096, 151936].  One input set
+    (17 GB of arena); each timed call still reads far more than the 256 MB
+    Infinity Cache holds."""
+    wl = W.long_context_workload()
+    max_keep = max(len(k) for k in wl.keep)
+    wl.capacity = (int(wl.prefix_len.max()) + 128 + max_keep * (iters + warmup + 2) + 63) // 64 * 64
+    plan = ops.plan_attention(wl.row_offset, wl.prefix_len, wl.num_q_heads, wl.num_kv_heads,
+                              wl.head_dim, 0).to(device)
+    q, kc, vc, kt, vt = wl.make_tensors(device, seed=300)
+    out = torch.empty_like(q)
+    meta = dict(
+        row_offset=torch.from_numpy(wl.row_offset).to(device),
+        prefix_start=torch.from_numpy(wl.prefix_start).to(device),
+        prefix_len=torch.from_numpy(wl.prefix_len.astype(np.int32)).to(device),
+        parent=torch.from_numpy(wl.parent_flat).to(device),
+    )
+    keep = np.full((wl.num_requests, max_keep), -1, np.int32)
+    for i, k in enumerate(wl.keep):
+        keep[i, :len(k)] = k
+    keep_rows = torch.from_numpy(keep).to(device)
+    keep_len = torch.from_numpy(np.asarray([len(k) for k in wl.keep], np.int32)).to(device)
+    lengths = meta["prefix_len"].clone()
+    ptrs = [ops.pointer_array([t], device) for t in (kc, vc, kt, vt)]
+
+    def attn(_):
+        ops.tree_attention(q, kc, vc, kt, vt, meta["row_offset"], meta["prefix_start"],
+                           meta["prefix_len"], meta["parent"], plan, out=out)
+
+    def commit(_):
+        ops.kv_commit(*ptrs, num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim,
+                      cache_head_stride=kc.stride(0), cache_token_stride=kc.stride(1),
+                      tree_row_stride=kt.stride(0), tree_head_stride=kt.stride(1),
+                      row_offset=meta["row_offset"], keep_rows=keep_rows, keep_len=keep_len,
+                      prefix_start=meta["prefix_start"], lengths=lengths, capacity=wl.capacity)
+
+    for k in range(warmup):
+        attn(k)
+    torch.cuda.synchronize()
+    attn_ms = time_calls(torch, attn, iters)
+    commit_ms = time_calls(torch, commit, iters)
+    del q, kc, vc, kt, vt, out, ptrs
+    torch.cuda.empty_cache()
+
+    # Sampling over every packed row of the wave.
+    vocab = 151936
+    gen = torch.Generator(device=device).manual_seed(301)
+    rows = wl.total_rows
+    logits = torch.randn((rows, vocab), generator=gen, device=device) * 3.0
+    depth = max(max(W.depths_of(p)) for p in wl.parents)
+    uniforms = torch.rand((wl.num_requests, 2 * (depth + 1)), generator=gen, device=device)
+    token = torch.from_numpy(np.concatenate(
+        [np.asarray([0] + list(t), np.int32) for t in wl.tokens])).to(device)
+    res = [None]
+
+    def sample(_):
+        res[0] = ops.tree_sample(logits, meta["row_offset"], meta["parent"], token, uniforms,
+                                 depth, out=res[0])
+
+    for k in range(2):
+        sample(k)
+    torch.cuda.synchronize()
+    samp_ms = time_calls(torch, sample, max(5, iters // 2))
+    del logits
+    torch.cuda.empty_cache()
+    attn_avg, commit_avg, samp_avg = (statistics.fmean(x) for x in (attn_ms, commit_ms, samp_ms))
+    abytes, sbytes = wl.algorithmic_bytes(), rows * vocab * 4
+    return {
+        "workload": "128 requests, prefixes log-uniform 8k-32k "
+                    f"({int(wl.prefix_len.sum())} tokens), {rows} rows, 32q/8kv, D128",
+        "attention": {"us_avg": attn_avg * 1e3, "us_median": statistics.median(attn_ms) * 1e3,
+                      "rows_per_s": rows / (attn_avg * 1e-3),
+                      "gbs": abytes / (attn_avg * 1e-3) / 1e9,
+                      "frac": abytes / (attn_avg * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                      "algorithmic_bytes": abytes, "plan_units": plan.units,
+                      "plan_merges": plan.merges},
+        "commit": {"us_avg": commit_avg * 1e3, "rows": int(sum(len(k) for k in wl.keep))},
+        "sampler": {"us_avg": samp_avg * 1e3, "nodes_per_s": rows / (samp_avg * 1e-3),
+                    "gbs": sbytes / (samp_avg * 1e-3) / 1e9,
+                    "frac": sbytes / (samp_avg * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                    "algorithmic_bytes": sbytes},
+    }
 
 
 def cpu_attention_baseline(torch, np, W, requests):
@@ -324,6 +414,10 @@ def main():
             "frac": sbytes / (savg * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "algorithmic_bytes": sbytes,
         }
+    if not args.no_long_context:
+        del sets
+        torch.cuda.empty_cache()
+        result["long_context"] = long_context_bench(torch, np, W, ops, device)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_attention_baseline(torch, np, W, args.cpu_requests)
         if samp_sets is not None:
