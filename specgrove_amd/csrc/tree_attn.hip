@@ -59,6 +59,7 @@ constexpr int kAncWords = kMaxTreeRows / 32;
 constexpr int kMergeThreads = 256;
 constexpr int32_t kPlanMagic = 0x53475041;  // "SGPA"
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLazyLog2 = 8.0f;  // softmax reference point moves after a 2^8 growth
 constexpr int kDefaultCUs = 256;
 
 struct PlanHeader {
@@ -427,16 +428,22 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
       s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kb], qf[kb], s, 0, 0, 0);
     return s;
   };
-  // Online softmax, step 1: new running max of the scores x (masked already);
-  // the state is rescaled only when some lane's max grew (rare after the
-  // first blocks).
+  // Online softmax, step 1: running max of the scores x (masked already).
+  // The reference point st.m moves only when some lane's max grew by more than
+  // kLazyLog2 in exp2 units: until then the probabilities exp2((x - m) * c2)
+  // may exceed 1 (at most 2^kLazyLog2, exact in fp32 and as bf16 MFMA
+  // operands), and the final division by the sum normalises them all the
+  // same.  With a 32-key block per window the max of one of 32 queries grows
+  // in most windows, so rescaling at every growth would cost 64 multiplies in
+  // most windows.
   auto softmax_max = [&](const float (&x)[16]) {
     float tmax = x[0];
 #pragma unroll
     for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, x[r]);
     tmax = half_max(tmax);
     const float m_new = fmaxf(st.m, tmax);
-    if (__ballot(m_new > st.m)) {
+    // st.m = -inf gives +inf here (rescale); both -inf gives NaN (keep).
+    if (__ballot((m_new - st.m) * c2 > kLazyLog2)) {
       const float alpha = (st.m == -__builtin_inff()) ? 0.0f
                                                        : __builtin_amdgcn_exp2f((st.m - m_new) * c2);
       st.l *= alpha;
