@@ -117,20 +117,25 @@ __device__ __forceinline__ float wave_butterfly_sum(float v) {
   return v;
 }
 
+typedef __attribute__((ext_vector_type(4))) float floatx4;
+
 // Lane l of the wave loads tokens 2048*s + 256*j + 4*l + c into v[4*j + c];
 // tokens at or beyond vocab read as -inf (they contribute E = 0).
-template <bool kVec4>
+template <bool kVec4, bool kStream = false>
 __device__ __forceinline__ void load_slab(const float* __restrict__ x, int vocab,
                                           int slab, int lane, float v[32]) {
   const int base = slab * kSlab + 4 * lane;
   if (kVec4 && (slab + 1) * kSlab <= vocab) {  // full slab: no bounds checks
 #pragma unroll
     for (int j = 0; j < kLinesPerSlab; ++j) {
-      const float4 q = *reinterpret_cast<const float4*>(x + base + kLine * j);
-      v[4 * j + 0] = q.x;
-      v[4 * j + 1] = q.y;
-      v[4 * j + 2] = q.z;
-      v[4 * j + 3] = q.w;
+      // Non-temporal: the statistics pass reads every row once.
+      const floatx4 q =
+          kStream ? __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(x + base + kLine * j))
+                  : *reinterpret_cast<const floatx4*>(x + base + kLine * j);
+      v[4 * j + 0] = q[0];
+      v[4 * j + 1] = q[1];
+      v[4 * j + 2] = q[2];
+      v[4 * j + 3] = q[3];
     }
   } else if (kVec4) {
 #pragma unroll
@@ -200,10 +205,10 @@ __global__ __launch_bounds__(kStatsThreads) void row_stats_kernel(
   constexpr int kWavesPerRow = kStatsThreads / kWave;
   float v[32], w[32];
   int s = wave;
-  if (s < slabs) load_slab<kVec4>(x, vocab, s, lane, v);
+  if (s < slabs) load_slab<kVec4, true>(x, vocab, s, lane, v);
   while (s < slabs) {
     const int next = s + kWavesPerRow;
-    if (next < slabs) load_slab<kVec4>(x, vocab, next, lane, w);
+    if (next < slabs) load_slab<kVec4, true>(x, vocab, next, lane, w);
     const MZ a = slab_stats(v);
     if (lane == 0) {
       s_m[s] = a.m;
@@ -211,7 +216,7 @@ __global__ __launch_bounds__(kStatsThreads) void row_stats_kernel(
     }
     if (next >= slabs) break;
     const int next2 = next + kWavesPerRow;
-    if (next2 < slabs) load_slab<kVec4>(x, vocab, next2, lane, v);
+    if (next2 < slabs) load_slab<kVec4, true>(x, vocab, next2, lane, v);
     const MZ b = slab_stats(w);
     if (lane == 0) {
       s_m[next] = b.m;
