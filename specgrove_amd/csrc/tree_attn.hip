@@ -132,18 +132,36 @@ __host__ __device__ constexpr int swz_v(int r) {
 }
 
 // 16-byte HBM -> LDS DMA of every lane: lane i's bytes at gbase + voff land at
-// LDS byte lds + 16*i.  K/V are streamed once per unit, so the loads carry the
-// non-temporal hint (nt): they do not displace reusable lines in the caches
-// (measured 3-6 % faster on the Qwen3-8B wave).  Issued as inline assembly so that the compiler does not
+// LDS byte lds + 16*i.  When a (request, kv head)'s K/V is read by one unit
+// only, the loads carry the non-temporal hint (nt) and do not displace
+// reusable lines in the caches (measured 3-7 % faster on the Qwen3-8B wave);
+// the row tiles of a larger tree re-read the same K/V and keep it cached.  Issued as inline assembly so that the compiler does not
 // model it: its automatic waits would otherwise stall the first LDS read of the
 // other pipeline stage on this in-flight copy.  The kernel waits for the DMAs
 // explicitly (s_waitcnt vmcnt(0)) before the barrier that publishes the tile.
 // m0 is written here; nothing else in the kernel reads m0.
+template <bool kStream>
 __device__ __forceinline__ void dma16(const void* gbase, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt"
-               :
-               : "s"(lds), "v"(voff), "s"(gbase)
-               : "memory");
+  if constexpr (kStream) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt"
+                 :
+                 : "s"(lds), "v"(voff), "s"(gbase)
+                 : "memory");
+  } else {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :
+                 : "s"(lds), "v"(voff), "s"(gbase)
+                 : "memory");
+  }
+}
+// Run-time choice for the unit's rare issue paths (prologue, partial and tree tiles).
+__device__ __forceinline__ void dma16(const void* gbase, uint32_t voff, uint32_t lds,
+                                      bool stream) {
+  if (stream) {
+    dma16<true>(gbase, voff, lds);
+  } else {
+    dma16<false>(gbase, voff, lds);
+  }
 }
 
 // s_waitcnt immediate that waits for vmcnt <= n and leaves the other counters
@@ -179,6 +197,8 @@ template <Mask M>
 using MaskTag = std::integral_constant<Mask, M>;
 template <int N>
 using IntTag = std::integral_constant<int, N>;
+template <bool B>
+using BoolTag = std::integral_constant<bool, B>;
 
 // Per-wave attention state: one query column per lane pair.
 template <int D>
@@ -239,6 +259,8 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
   const int64_t row = static_cast<int64_t>(r0) + u.row_begin + r_local;
   const int g = u.kv_head;
   const bool do_tree = (u.flags & 1) != 0;
+  // The request's K/V is read by this unit alone when its rows fit one row tile.
+  const bool stream_kv = n * G <= kQPerUnit;
 
   // Ancestor-or-self bitsets of the tile's rows (request-local numbering).
   if (do_tree) {
@@ -310,7 +332,8 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
       const unsigned char* base = reinterpret_cast<const unsigned char*>(
           (is_v ? vc : kc) + static_cast<int64_t>(t) * kTileKeys * cstride);
 #pragma unroll
-      for (int i = 0; i < DMAS; ++i) dma16(base, is_v ? v_dma[i] : k_dma[i], dst + 1024 * i);
+      for (int i = 0; i < DMAS; ++i)
+        dma16(base, is_v ? v_dma[i] : k_dma[i], dst + 1024 * i, stream_kv);
       return;
     }
     const bool tree = t >= tiles_prefix;
@@ -328,7 +351,8 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
       // score mask (K) or a zero probability (V) removes.
       const int key = is_v ? min(lds_row, last) : min((lds_row & ~31) + key_pi(lds_row & 31), last);
       const int sw = is_v ? swz_v<D>(lds_row) : swz_k<D>(lds_row);
-      dma16(base, static_cast<uint32_t>(2 * (key * stride + 8 * (phys ^ sw))), dst + 1024 * i);
+      dma16(base, static_cast<uint32_t>(2 * (key * stride + 8 * (phys ^ sw))), dst + 1024 * i,
+            stream_kv);
     }
   };
 
@@ -526,9 +550,10 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
   const int64_t tile_bytes = static_cast<int64_t>(kTileKeys) * cstride * 2;
   const uint32_t k_lds_wave = lds_addr(s_k) + wave * DMAS * 1024;
   const uint32_t v_lds_wave = lds_addr(s_v) + wave * DMAS * 1024;
-  auto fast_window = [&](int i, auto per_tag, auto cur_tag) {
+  auto fast_window = [&](int i, auto per_tag, auto cur_tag, auto stream_tag) {
     constexpr int PER = decltype(per_tag)::value;  // tiles per window
     constexpr int kCur = decltype(cur_tag)::value;  // ring stage of group i's first tile
+    constexpr bool kStream = decltype(stream_tag)::value;
     constexpr int LK = kStages / PER;
     // per_iter 1: windows i-2 and i-1 each issued one K and one V tile.
     wait_halves(PER == 1 ? 4 : 0);
@@ -541,11 +566,11 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
     for (int k = 0; k < PER; ++k) {
 #pragma unroll
       for (int d = 0; d < DMAS; ++d)
-        dma16(vb + k * tile_bytes, v_dma[d],
+        dma16<kStream>(vb + k * tile_bytes, v_dma[d],
               v_lds_wave + ((kCur + kStages - PER + k) % kStages) * STAGEB + 1024 * d);
 #pragma unroll
       for (int d = 0; d < DMAS; ++d)
-        dma16(kb + k * tile_bytes, k_dma[d],
+        dma16<kStream>(kb + k * tile_bytes, k_dma[d],
               k_lds_wave + ((kCur + k) % kStages) * STAGEB + 1024 * d);
     }
   };
@@ -575,9 +600,11 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
   int i = 0;
   bf16x8 pf[2];
   if (per_iter == 2) {
+    // 1-2 q-groups: at most 64 query vectors, the request's rows fit one row
+    // tile, so the unit is its K/V's only reader.
     auto step = [&](int w, auto cur_tag, auto next_tag) {
       if (w < fast_end) {
-        fast_window(w, IntTag<2>{}, cur_tag);
+        fast_window(w, IntTag<2>{}, cur_tag, BoolTag<true>{});
       } else {
         window(w);
       }
@@ -589,21 +616,30 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
       step(i + 1, IntTag<2>{}, IntTag<0>{});
     }
   } else if (!lag) {
-    auto step = [&](int w, auto cur_tag) {
+    auto step = [&](int w, auto cur_tag, auto stream_tag) {
       constexpr int kCur = decltype(cur_tag)::value;
       if (w < fast_end) {
-        fast_window(w, IntTag<1>{}, cur_tag);
+        fast_window(w, IntTag<1>{}, cur_tag, stream_tag);
       } else {
         window(w);
       }
       softmax_qk((kCur + 1) % kStages, pf);
       pv(pf, kCur);
     };
-    for (; i + 4 <= steady_end; i += 4) {
-      step(i, IntTag<0>{});
-      step(i + 1, IntTag<1>{});
-      step(i + 2, IntTag<2>{});
-      step(i + 3, IntTag<3>{});
+    if (stream_kv) {
+      for (; i + 4 <= steady_end; i += 4) {
+        step(i, IntTag<0>{}, BoolTag<true>{});
+        step(i + 1, IntTag<1>{}, BoolTag<true>{});
+        step(i + 2, IntTag<2>{}, BoolTag<true>{});
+        step(i + 3, IntTag<3>{}, BoolTag<true>{});
+      }
+    } else {
+      for (; i + 4 <= steady_end; i += 4) {
+        step(i, IntTag<0>{}, BoolTag<false>{});
+        step(i + 1, IntTag<1>{}, BoolTag<false>{});
+        step(i + 2, IntTag<2>{}, BoolTag<false>{});
+        step(i + 3, IntTag<3>{}, BoolTag<false>{});
+      }
     }
   } else if (steady_end > 0) {
     // Lagging stream: PV of the previous window's probabilities first.
