@@ -944,8 +944,22 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
   const int64_t bins = std::min<int64_t>(target, static_cast<int64_t>(units.size()));
   std::vector<int64_t> load(bins, 0);
   std::vector<std::vector<size_t>> bin_units(bins);
+  // Units that read the same (request, kv head) K/V (the row tiles of a tree
+  // larger than one tile, and split pieces) go to lists of one XCD: the
+  // dispatcher places workgroup b on XCD b % 8, whose L2 then serves the
+  // re-reads.  (A placement heuristic only.)
+  constexpr int64_t kXcds = 8;
+  std::vector<int64_t> xcd_of(static_cast<size_t>(num_requests) * num_kv_heads, -1);
   for (size_t k : order) {
-    const int64_t b = std::min_element(load.begin(), load.end()) - load.begin();
+    const size_t key = static_cast<size_t>(units[k].req) * num_kv_heads + units[k].kv_head;
+    int64_t b = -1;
+    if (xcd_of[key] >= 0 && bins >= kXcds) {
+      for (int64_t c = xcd_of[key]; c < bins; c += kXcds)
+        if (b < 0 || load[c] < load[b]) b = c;
+    } else {
+      b = std::min_element(load.begin(), load.end()) - load.begin();
+      xcd_of[key] = b % kXcds;
+    }
     load[b] += cost[k];
     bin_units[b].push_back(k);
   }
