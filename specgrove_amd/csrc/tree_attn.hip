@@ -360,18 +360,15 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
   // groups-1 each consume one group of per_iter tiles: the PV products of
   // group i and the QK products of group i+1 (one group ahead, so that the QK
   // MFMAs overlap the softmax VALU work).  Window j issues the V tiles of
-  // group j+lv and then the K tiles of group j+lk.
-  //   per_iter 1: lk 4, lv 2.  The waves of key stream 1 run half a window
-  //     behind stream 0 (PV of group i-1 first, then the QK/softmax of group
-  //     i), so the two waves sharing a SIMD alternate between MFMA-heavy and
-  //     VALU/LDS-heavy phases.  Window i reads K(i+1), V(i) and V(i-1); the
-  //     ring keeps 2.5 tiles in flight.
-  //   per_iter 2: lk 2, lv 1, no lag; one group (two tiles) in flight.
+  // group j+lv and then the K tiles of group j+lk, into the ring slots that
+  // window j-1 finished reading.
+  //   per_iter 1 (3-4 q-groups): lk 4, lv 3.  Window i reads K(i+1) and
+  //     V(i); the tiles of windows i-2 and i-1 may still be in flight.
+  //   per_iter 2 (1-2 q-groups, two key streams): lk 2, lv 1; window i reads
+  //     the groups window i-1 issued, so nothing may be in flight.
   const int groups = (tiles + per_iter - 1) / per_iter;
-  const bool pingpong = false;
-  const bool lag = pingpong && ks == 1;
   const int lk = kStages / per_iter;
-  const int lv = pingpong ? 2 : lk - 1;
+  const int lv = lk - 1;
   auto group_tiles = [&](int grp) {
     return grp < 0 ? 0 : max(0, min(per_iter, tiles - grp * per_iter));
   };
@@ -398,12 +395,9 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
   // i-2 and all of window i-1 may still be in flight.  per_iter 2: both come
   // from window i-1, the latest window, so nothing may be in flight.
   auto newer_before = [&](int i) {
-    if (!pingpong) {
-      int c = 0;
-      for (int j = i + 2 - lk; j < i; ++j) c += group_tiles(j + lv) + group_tiles(j + lk);
-      return c;
-    }
-    return group_tiles(i + 2) + group_tiles(i + 1) + group_tiles(i + 3);
+    int c = 0;
+    for (int j = i + 2 - lk; j < i; ++j) c += group_tiles(j + lv) + group_tiles(j + lk);
+    return c;
   };
 
   // Lane parts of the LDS read addresses (bytes), including this wave's tile
@@ -523,10 +517,7 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
   // which needs K(0) from window -lk; everything issued after it may be in
   // flight: V(0), V(1), K(1), K(2), K(3) (per_iter 1) or V(0), K(1) (per_iter 2).
   for (int j = -lk; j < 0; ++j) issue(j);
-  if (pingpong) {
-    wait_halves(group_tiles(0) + group_tiles(1) + group_tiles(1) + group_tiles(2) +
-                group_tiles(3));
-  } else {
+  {
     int newer = 0;
     for (int j = 1 - lk; j < 0; ++j) newer += group_tiles(j + lv) + group_tiles(j + lk);
     wait_halves(newer);
@@ -615,7 +606,7 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
       step(i, IntTag<0>{}, IntTag<2>{});
       step(i + 1, IntTag<2>{}, IntTag<0>{});
     }
-  } else if (!lag) {
+  } else {
     auto step = [&](int w, auto cur_tag, auto stream_tag) {
       constexpr int kCur = decltype(cur_tag)::value;
       if (w < fast_end) {
@@ -641,26 +632,6 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
         step(i + 3, IntTag<3>{}, BoolTag<false>{});
       }
     }
-  } else if (steady_end > 0) {
-    // Lagging stream: PV of the previous window's probabilities first.
-    auto step = [&](int w, auto cur_tag) {
-      constexpr int kCur = decltype(cur_tag)::value;
-      window(w);
-      pv(pf, (kCur + kStages - 1) % kStages);
-      softmax_qk((kCur + 1) % kStages, pf);
-    };
-    window(0);
-    softmax_qk(1, pf);
-    i = 1;
-    for (; i + 4 <= steady_end; i += 4) {
-      step(i, IntTag<1>{});
-      step(i + 1, IntTag<2>{});
-      step(i + 2, IntTag<3>{});
-      step(i + 3, IntTag<0>{});
-    }
-    // Catch up before the unlagged windows: PV of window i-1 (its V tile stays
-    // in the ring until window i+1 issues).
-    pv(pf, (i - 1) % kStages);
   }
   // Remaining windows: runtime stages, masks from the key limit and the
   // ancestor bitsets.
