@@ -95,6 +95,16 @@ def test_qwen_vocab_bit_exact(device, oracle):
     assert gpu["accept_len"].max() >= 1
 
 
+def test_long_context_trees_bit_exact(device, oracle):
+    """The long-context wave's 128 trees (1 to 128 nodes, canonical, depth up
+    to 16) with every packed row sampled, at vocabulary 8192."""
+    wl = W.long_context_workload()
+    case = tree_problem(31, len(wl.parents), None, 8192, trees=wl.parents, child_boost=10.0)
+    assert case["logits"].shape[0] == wl.total_rows == 4096
+    gpu = _check_case(case, device, oracle)
+    assert gpu["accept_len"].max() >= 3
+
+
 def test_golden_fixture(device):
     from pathlib import Path
     path = Path(__file__).parent / "golden" / "sampler_tiny.npz"
