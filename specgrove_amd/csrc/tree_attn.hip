@@ -721,10 +721,21 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
     }
     return;
   }
-  if (!q_valid) return;
+  // Output through a per-wave LDS staging tile: each lane holds 64 scattered
+  // head dims of one query vector, while HBM wants each query vector's D
+  // contiguous values written whole.  The tile (32 query vectors, rows padded
+  // by 16 bytes against bank conflicts) lies in ring space this wave alone
+  // uses now: with two key streams behind the stream-merge slot of its ring,
+  // otherwise in one of the four quarters of the rings.
+  constexpr int kRowBytes = 2 * D;
+  constexpr int kPitch = kRowBytes + 16;
+  constexpr int kSlotBytes = STATE * 64 * 4;
+  static_assert(kSlotBytes + 32 * kPitch <= kStages * STAGEB &&
+                    2 * 32 * kPitch <= kStages * STAGEB,
+                "output staging must fit the rings");
+  unsigned char* stage =
+      ((qg & 1) ? s_v : s_k) + (streams > 1 ? kSlotBytes : (qg >> 1) * 32 * kPitch);
   const float inv = st.l > 0.0f ? 1.0f / st.l : 0.0f;
-  uint16_t* op = static_cast<uint16_t*>(a.out_dev) + row * a.out_row_stride +
-                 static_cast<int64_t>(head) * a.out_head_stride + 4 * half;
 #pragma unroll
   for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -732,8 +743,28 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
       uint2 packed;
       packed.x = pack_bf16x2(st.acc[db][4 * q4] * inv, st.acc[db][4 * q4 + 1] * inv);
       packed.y = pack_bf16x2(st.acc[db][4 * q4 + 2] * inv, st.acc[db][4 * q4 + 3] * inv);
-      *reinterpret_cast<uint2*>(op + 32 * db + 8 * q4) = packed;
+      *reinterpret_cast<uint2*>(stage + col * kPitch + 2 * (32 * db + 8 * q4 + 4 * half)) =
+          packed;
     }
+  __builtin_amdgcn_wave_barrier();
+  // Row-contiguous read-back (LDS keeps this wave's accesses in order): every
+  // store instruction writes 512 contiguous bytes of whole query vectors.
+#pragma unroll
+  for (int i = 0; i < 32 * kRowBytes / 512; ++i) {
+    const int linear = i * 512 + 8 * lane;
+    const int q = linear / kRowBytes;  // query vector of this q-group
+    const int within = linear - q * kRowBytes;
+    const uint2 v = *reinterpret_cast<const uint2*>(stage + q * kPitch + within);
+    const int mq = qg * 32 + q;
+    const int rq = mq / G;
+    if (rq < u.row_count) {
+      uint16_t* dst = static_cast<uint16_t*>(a.out_dev) +
+                      (static_cast<int64_t>(r0) + u.row_begin + rq) * a.out_row_stride +
+                      static_cast<int64_t>(u.kv_head * G + (mq - rq * G)) * a.out_head_stride +
+                      within / 2;
+      *reinterpret_cast<uint2*>(dst) = v;
+    }
+  }
 }
 
 // One workgroup per work list (one per CU): the units of list b are
