@@ -61,6 +61,7 @@ constexpr int32_t kPlanMagic = 0x53475041;  // "SGPA"
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazyLog2 = 8.0f;  // softmax reference point moves after a 2^8 growth
 constexpr int kDefaultCUs = 256;
+constexpr int64_t kSplitAbovePercent = 150;  // planner: split units above 1.5x a mean list
 
 struct PlanHeader {
   int32_t magic;
@@ -104,6 +105,10 @@ struct MergeGroup {
 
 __host__ __device__ constexpr size_t partial_floats(int head_dim) {
   return static_cast<size_t>(kQPerUnit) * (head_dim + 2);
+}
+
+__host__ __device__ constexpr int merge_blocks_per_group(int head_dim) {
+  return (head_dim / 4) * kQPerUnit / kMergeThreads;
 }
 
 // LDS row of key k inside its 32-key block (inverse of pi).
@@ -748,21 +753,39 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
     }
   __builtin_amdgcn_wave_barrier();
   // Row-contiguous read-back (LDS keeps this wave's accesses in order): every
-  // store instruction writes 512 contiguous bytes of whole query vectors.
-#pragma unroll
-  for (int i = 0; i < 32 * kRowBytes / 512; ++i) {
-    const int linear = i * 512 + 8 * lane;
-    const int q = linear / kRowBytes;  // query vector of this q-group
-    const int within = linear - q * kRowBytes;
-    const uint2 v = *reinterpret_cast<const uint2*>(stage + q * kPitch + within);
+  // store instruction writes 1 KiB of whole query vectors, 16 bytes a lane when
+  // the output strides allow it (multiples of 8 elements), else 8 bytes a lane.
+  uint16_t* const out_base = static_cast<uint16_t*>(a.out_dev) +
+                             (static_cast<int64_t>(r0) + u.row_begin) * a.out_row_stride +
+                             static_cast<int64_t>(u.kv_head * G) * a.out_head_stride;
+  auto dst_of = [&](int q, int within) {
     const int mq = qg * 32 + q;
     const int rq = mq / G;
-    if (rq < u.row_count) {
-      uint16_t* dst = static_cast<uint16_t*>(a.out_dev) +
-                      (static_cast<int64_t>(r0) + u.row_begin + rq) * a.out_row_stride +
-                      static_cast<int64_t>(u.kv_head * G + (mq - rq * G)) * a.out_head_stride +
-                      within / 2;
-      *reinterpret_cast<uint2*>(dst) = v;
+    return rq < u.row_count
+               ? out_base + static_cast<int64_t>(rq) * a.out_row_stride +
+                     static_cast<int64_t>(mq - rq * G) * a.out_head_stride + within / 2
+               : nullptr;
+  };
+  if (((a.out_row_stride | a.out_head_stride) & 7) == 0 &&
+      (reinterpret_cast<uintptr_t>(a.out_dev) & 15) == 0) {
+#pragma unroll
+    for (int i = 0; i < 32 * kRowBytes / 1024; ++i) {
+      const int linear = i * 1024 + 16 * lane;
+      const int q = linear / kRowBytes;  // query vector of this q-group
+      const int within = linear - q * kRowBytes;
+      const uint4 v = *reinterpret_cast<const uint4*>(stage + q * kPitch + within);
+      uint16_t* dst = dst_of(q, within);
+      if (dst != nullptr) *reinterpret_cast<uint4*>(dst) = v;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 32 * kRowBytes / 512; ++i) {
+      const int linear = i * 512 + 8 * lane;
+      const int q = linear / kRowBytes;
+      const int within = linear - q * kRowBytes;
+      const uint2 v = *reinterpret_cast<const uint2*>(stage + q * kPitch + within);
+      uint16_t* dst = dst_of(q, within);
+      if (dst != nullptr) *reinterpret_cast<uint2*>(dst) = v;
     }
   }
 }
@@ -783,21 +806,25 @@ __global__ __launch_bounds__(kThreads, kListsPerCU) void tree_attn_kernel(SgTree
   }
 }
 
-// Combines the partials of one split group: thread -> (query vector, float4 chunk).
+// Combines the partials of the split groups: merge_blocks_per_group(D)
+// workgroups per group, thread -> one (query vector, float4 chunk).
 template <int D>
 __global__ __launch_bounds__(kMergeThreads) void tree_attn_merge_kernel(SgTreeAttnArgs a) {
   const PlanHeader* hdr = static_cast<const PlanHeader*>(a.plan_dev);
+  constexpr int CH = D / 4;  // float4 chunks per query vector
+  const int sub = blockIdx.x % merge_blocks_per_group(D);
   const MergeGroup grp = reinterpret_cast<const MergeGroup*>(
-      reinterpret_cast<const AttnUnit*>(hdr + 1) + hdr->num_units)[blockIdx.x];
+      reinterpret_cast<const AttnUnit*>(hdr + 1) +
+      hdr->num_units)[blockIdx.x / merge_blocks_per_group(D)];
   const int G = a.num_q_heads / a.num_kv_heads;
   const int r0 = a.row_offset_dev[grp.req];
   const float* ws = static_cast<const float*>(a.workspace_dev);
-  constexpr int CH = D / 4;  // float4 chunks per query vector
   const int vectors = grp.row_count * G;
-  for (int item = threadIdx.x; item < CH * kQPerUnit; item += kMergeThreads) {
+  {
+    const int item = sub * kMergeThreads + static_cast<int>(threadIdx.x);
     const int ch = item / kQPerUnit;  // chunk index ((db*4 + q4)*2 + half)
     const int m = item - ch * kQPerUnit;
-    if (m >= vectors) continue;
+    if (m >= vectors) return;
     float mx = -__builtin_inff();
     for (int s = 0; s < grp.num_partials; ++s)
       mx = fmaxf(mx, ws[partial_floats(D) * (grp.first_partial + s) +
@@ -878,6 +905,32 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
     chunk = per_unit * kTileKeys;
   }
 
+  // Balance: a unit costing more than kSplitAbovePercent % of the mean work
+  // list is split over its prefix into pieces below that bound, so that the
+  // lists can be packed evenly (each split costs a partial write and a merge).
+  auto unit_cost = [&](int row_count, int64_t tiles) -> int64_t {
+    const int nq = (row_count * G + 31) / 32;
+    return nq <= 2 ? 550 + 57 * tiles : 840 + 88 * tiles;
+  };
+  std::vector<int> balance_splits(num_requests, 1);
+  {
+    int64_t total_cost = 0;
+    std::vector<int64_t> req_cost(num_requests, 0);
+    for (int i = 0; i < num_requests; ++i) {
+      const int rows = row_offset_host[i + 1] - row_offset_host[i];
+      const int64_t tiles = (prefix_len_host[i] + kTileKeys - 1) / kTileKeys +
+                            (rows + kTileKeys - 1) / kTileKeys;
+      for (int rb = 0; rb < rows; rb += rows_per_tile) {
+        const int64_t c = unit_cost(std::min(rows_per_tile, rows - rb), tiles);
+        total_cost += c * num_kv_heads;
+        req_cost[i] = std::max(req_cost[i], c);
+      }
+    }
+    const int64_t lists = std::max<int64_t>(1, std::min(target, base_units));
+    const int64_t bound = std::max<int64_t>(1, total_cost * kSplitAbovePercent / (100 * lists));
+    for (int i = 0; i < num_requests; ++i)
+      if (req_cost[i] > bound) balance_splits[i] = static_cast<int>((req_cost[i] + bound - 1) / bound);
+  }
   std::vector<AttnUnit> units;
   std::vector<MergeGroup> merges;
   int32_t partials = 0;
@@ -885,7 +938,11 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
     const int rows = row_offset_host[i + 1] - row_offset_host[i];
     if (rows == 0) continue;
     const int L = prefix_len_host[i];
-    const int splits = static_cast<int>(std::max<int64_t>(1, (L + chunk / 2) / chunk));
+    // Pieces keep at least four full tiles of prefix.
+    const int splits = std::max(1, std::min(std::max(balance_splits[i],
+                                                     static_cast<int>(std::max<int64_t>(
+                                                         1, (L + chunk / 2) / chunk))),
+                                            L / (4 * kTileKeys)));
     const int tiles = (rows + rows_per_tile - 1) / rows_per_tile;
     for (int g = 0; g < num_kv_heads; ++g) {
       for (int tile = 0; tile < tiles; ++tile) {
@@ -936,27 +993,31 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
     const int64_t tiles =
         (units[k].key_end - units[k].key_begin + kTileKeys - 1) / kTileKeys +
         ((units[k].flags & 1) ? (rows + kTileKeys - 1) / kTileKeys : 0);
-    const int nq = (units[k].row_count * G + 31) / 32;
-    cost[k] = nq <= 2 ? 550 + 57 * tiles : 840 + 88 * tiles;
+    cost[k] = unit_cost(units[k].row_count, tiles);
   }
   std::vector<size_t> order(units.size());
   std::iota(order.begin(), order.end(), size_t{0});
   std::stable_sort(order.begin(), order.end(),
                    [&](size_t x, size_t y) { return cost[x] > cost[y]; });
   const int64_t bins = std::min<int64_t>(target, static_cast<int64_t>(units.size()));
-  std::vector<int64_t> load(bins, 0);
-  std::vector<std::vector<size_t>> bin_units(bins);
+  // Units are first packed onto CUs (pairs of lists c and c + bins/2, which
+  // dispatch order places on one CU: every CU's first slot is filled before
+  // any second slot), then split between the CU's two workgroups.
+  constexpr int64_t kXcds = 8;
+  const bool paired = kListsPerCU == 2 && bins % (2 * kXcds) == 0;
+  const int64_t lpt_bins = paired ? bins / 2 : bins;
+  std::vector<int64_t> load(lpt_bins, 0);
+  std::vector<std::vector<size_t>> bin_units(lpt_bins);
   // Units that read the same (request, kv head) K/V (the row tiles of a tree
   // larger than one tile, and split pieces) go to lists of one XCD: the
   // dispatcher places workgroup b on XCD b % 8, whose L2 then serves the
   // re-reads.  (A placement heuristic only.)
-  constexpr int64_t kXcds = 8;
   std::vector<int64_t> xcd_of(static_cast<size_t>(num_requests) * num_kv_heads, -1);
   for (size_t k : order) {
     const size_t key = static_cast<size_t>(units[k].req) * num_kv_heads + units[k].kv_head;
     int64_t b = -1;
-    if (xcd_of[key] >= 0 && bins >= kXcds) {
-      for (int64_t c = xcd_of[key]; c < bins; c += kXcds)
+    if (xcd_of[key] >= 0 && lpt_bins >= kXcds) {
+      for (int64_t c = xcd_of[key]; c < lpt_bins; c += kXcds)
         if (b < 0 || load[c] < load[b]) b = c;
     } else {
       b = std::min_element(load.begin(), load.end()) - load.begin();
@@ -967,7 +1028,7 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
   }
   // Local search: move a unit out of the most loaded list, or swap it with a
   // smaller unit of the least loaded list, while that lowers the maximum.
-  for (int round = 0; bins > 1 && round < 4096; ++round) {
+  for (int round = 0; lpt_bins > 1 && round < 4096; ++round) {
     const int64_t hi = std::max_element(load.begin(), load.end()) - load.begin();
     const int64_t lo = std::min_element(load.begin(), load.end()) - load.begin();
     const int64_t gap = load[hi] - load[lo];
@@ -991,6 +1052,29 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
     }
     load[hi] -= best;
     load[lo] += best;
+  }
+  if (paired) {
+    // The CU's first-dispatched workgroup is older and wins its issue
+    // arbitration: measured on MI355X with equal lists, the second one takes
+    // 1.22x as long.  The first list gets the larger share, 55:45.
+    constexpr int64_t kFirstShare = 55, kSecondShare = 45;
+    std::vector<std::vector<size_t>> lists(bins);
+    for (int64_t c = 0; c < lpt_bins; ++c) {
+      std::vector<size_t>& us = bin_units[c];
+      std::stable_sort(us.begin(), us.end(),
+                       [&](size_t x, size_t y) { return cost[x] > cost[y]; });
+      int64_t l0 = 0, l1 = 0;
+      for (size_t k : us) {
+        if ((l0 + cost[k]) * kSecondShare <= (l1 + cost[k]) * kFirstShare) {
+          lists[c].push_back(k);
+          l0 += cost[k];
+        } else {
+          lists[c + lpt_bins].push_back(k);
+          l1 += cost[k];
+        }
+      }
+    }
+    bin_units = std::move(lists);
   }
 
   const size_t bytes = sizeof(PlanHeader) + sizeof(AttnUnit) * units.size() +
@@ -1055,7 +1139,8 @@ extern "C" int sg_tree_attn_fwd(const SgTreeAttnArgs* args, sg_stream_t stream) 
     hipLaunchKernelGGL(tree_attn_kernel<128>, dim3(a.plan_units), dim3(kThreads), 0, s, a);
     SG_LAUNCH_CHECK();
     if (a.plan_merges > 0) {
-      hipLaunchKernelGGL(tree_attn_merge_kernel<128>, dim3(a.plan_merges), dim3(kMergeThreads),
+      hipLaunchKernelGGL(tree_attn_merge_kernel<128>,
+                         dim3(a.plan_merges * merge_blocks_per_group(128)), dim3(kMergeThreads),
                          0, s, a);
       SG_LAUNCH_CHECK();
     }
@@ -1063,7 +1148,8 @@ extern "C" int sg_tree_attn_fwd(const SgTreeAttnArgs* args, sg_stream_t stream) 
     hipLaunchKernelGGL(tree_attn_kernel<64>, dim3(a.plan_units), dim3(kThreads), 0, s, a);
     SG_LAUNCH_CHECK();
     if (a.plan_merges > 0) {
-      hipLaunchKernelGGL(tree_attn_merge_kernel<64>, dim3(a.plan_merges), dim3(kMergeThreads),
+      hipLaunchKernelGGL(tree_attn_merge_kernel<64>,
+                         dim3(a.plan_merges * merge_blocks_per_group(64)), dim3(kMergeThreads),
                          0, s, a);
       SG_LAUNCH_CHECK();
     }
