@@ -825,23 +825,50 @@ __global__ __launch_bounds__(kMergeThreads) void tree_attn_merge_kernel(SgTreeAt
     const int ch = item / kQPerUnit;  // chunk index ((db*4 + q4)*2 + half)
     const int m = item - ch * kQPerUnit;
     if (m >= vectors) return;
+    // Every partial's (max, sum, O chunk) is loaded before any is used, so the
+    // group costs one memory round trip (up to kMergeBatch partials at a time).
+    constexpr int kMergeBatch = 4;
+    const float* part0 = ws + partial_floats(D) * grp.first_partial;
     float mx = -__builtin_inff();
-    for (int s = 0; s < grp.num_partials; ++s)
-      mx = fmaxf(mx, ws[partial_floats(D) * (grp.first_partial + s) +
-                        static_cast<size_t>(kQPerUnit) * D + m]);
-    const float m_use = (mx == -__builtin_inff()) ? 0.0f : mx;
     float l = 0.0f;
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s = 0; s < grp.num_partials; ++s) {
-      const float* part = ws + partial_floats(D) * (grp.first_partial + s);
-      const float ms = part[static_cast<size_t>(kQPerUnit) * D + m];
-      const float w = (ms == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(ms - m_use);
-      l += w * part[static_cast<size_t>(kQPerUnit) * D + kQPerUnit + m];
-      const float4 v = reinterpret_cast<const float4*>(part)[ch * kQPerUnit + m];
-      o.x += w * v.x;
-      o.y += w * v.y;
-      o.z += w * v.z;
-      o.w += w * v.w;
+    for (int s0 = 0; s0 < grp.num_partials; s0 += kMergeBatch) {
+      float ms[kMergeBatch], ls[kMergeBatch];
+      float4 vs[kMergeBatch];
+#pragma unroll
+      for (int j = 0; j < kMergeBatch; ++j) {
+        ms[j] = -__builtin_inff();
+        ls[j] = 0.0f;
+        vs[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (s0 + j < grp.num_partials) {
+          const float* part = part0 + partial_floats(D) * (s0 + j);
+          ms[j] = part[static_cast<size_t>(kQPerUnit) * D + m];
+          ls[j] = part[static_cast<size_t>(kQPerUnit) * D + kQPerUnit + m];
+          vs[j] = reinterpret_cast<const float4*>(part)[ch * kQPerUnit + m];
+        }
+      }
+      float bmx = mx;
+#pragma unroll
+      for (int j = 0; j < kMergeBatch; ++j) bmx = fmaxf(bmx, ms[j]);
+      const float m_use = (bmx == -__builtin_inff()) ? 0.0f : bmx;
+      // Rescale what earlier batches accumulated to the new reference.
+      const float w_old = (mx == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(mx - m_use);
+      l *= w_old;
+      o.x *= w_old;
+      o.y *= w_old;
+      o.z *= w_old;
+      o.w *= w_old;
+#pragma unroll
+      for (int j = 0; j < kMergeBatch; ++j) {
+        const float w =
+            (ms[j] == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(ms[j] - m_use);
+        l += w * ls[j];
+        o.x += w * vs[j].x;
+        o.y += w * vs[j].y;
+        o.z += w * vs[j].z;
+        o.w += w * vs[j].w;
+      }
+      mx = bmx;
     }
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     const int r_local = m / G;
