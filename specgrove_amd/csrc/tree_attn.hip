@@ -8,27 +8,27 @@
 // reference's dense packed mask (continuous_tree_block_decode.py:500-546 and
 // tree.py:19-26) evaluated without materialising the mask or copying prefixes.
 //
-// Decomposition (MI355X, one 8-wave workgroup per CU):
+// Decomposition (MI355X, two 4-wave workgroups per CU):
 //   unit      = (request, kv head, tile of up to 128/G query rows = 128 query
 //               vectors = four 32-vector q-groups, range of prefix keys); the
 //               unit that ends a request's key range also covers its tree rows;
-//   iteration = one 128-key tile of K and V moved HBM -> LDS by
-//               global_load_lds_dwordx4 (no register staging), double-buffered,
-//               split into four 32-key blocks;
-//   wave      = one q-group x a subset of the tile's key blocks: with 3-4
-//               q-groups two waves share a q-group (two blocks each), with 1-2
-//               q-groups four waves share it (one block each).  Every wave runs
-//               its own online softmax; the waves of a q-group are merged
-//               through LDS at the end, so the serial chain of a unit is a
-//               quarter or half of its keys per wave.
+//   work list = the units one workgroup runs in order; the host planner packs
+//               units onto lists (lists c and c + 256 share a CU);
+//   window    = one barrier; consumes one group of 32-key K and V tiles, moved
+//               HBM -> LDS by global_load_lds_dwordx4 (no register staging)
+//               into 4-tile rings issued two to four windows ahead;
+//   wave      = one q-group over every tile (3-4 q-groups) or one of two key
+//               streams of a q-group taking alternate tiles (1-2 q-groups).
+//               Every wave runs its own online softmax; the key streams of a
+//               q-group are merged through LDS at the end of the unit.
 // Per 32-key block a wave computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16
 // (A = K rows from LDS stored in the permuted order pi, so the result gives
 // each lane 16 consecutive keys; B = Q in registers) and O^T += V^T P^T with
 // the same MFMA (A = V read transposed from row-major LDS by ds_read_b64_tr_b16,
 // B = P in registers).  LDS rows are unpadded; the 16-byte chunk c of row r is
 // stored at chunk c ^ swz(r) so that both read patterns are bank-conflict free.
-// Split key ranges (only when a wave has fewer units than CUs) leave
-// unnormalised partials that a second kernel combines.
+// Split key ranges (units far above a mean list, or waves with fewer units
+// than lists) leave unnormalised partials that a second kernel combines.
 #include <algorithm>
 #include <climits>
 #include <cstring>
