@@ -176,7 +176,7 @@ typedef struct SgTreeSampleArgs {
   int32_t* keep_rows_dev;        /* optional [n, max_depth+1]: [0] + nodes, -1 padded */
   int32_t* status_dev;           /* optional [1]: SG_EINVAL if a walk broke the contract */
   void* workspace_dev;           /* >= sg_tree_sample_workspace_bytes(): per-slab
-                                    complement totals of the exit rows */
+                                    and per-line complement totals of the exit rows */
   size_t workspace_bytes;
 } SgTreeSampleArgs;
 

@@ -73,10 +73,12 @@ __device__ __forceinline__ float sg_exp(float x) {
 
 // E(x) for x <= 0 (every argument of the form value - max): the same
 // operations as sg_exp without the upper clamp and overflow select, which
-// cannot apply there, so the results are identical.
+// cannot apply there, and without the lower clamp: it leaves every live x
+// (x >= -87) unchanged, and the final select returns 0 for the others
+// whatever the polynomial gave them.  The results are identical.
 __device__ __forceinline__ float sg_exp_nonpos(float x) {
   const bool live = x >= -87.0f;
-  const float xc = fmaxf(x, -87.0f);
+  const float xc = x;
   const float n = __builtin_rintf(xc * SG_LOG2E);
   float r = __builtin_fmaf(-n, SG_LN2_HI, xc);
   r = __builtin_fmaf(-n, SG_LN2_LO, r);
@@ -298,8 +300,6 @@ struct RouteShared {
   float rz[kMaxTreeRows];
   float u[2 * kMaxTreeRows + 2];
   int child_tok[kMaxTreeRows];  // children of the exit node, ascending node order
-  int first_child[kMaxTreeRows];   // smallest child of node v, -1 for a leaf
-  int next_sibling[kMaxTreeRows];  // next larger node with the same parent, -1 if none
   int child_count;
   int exit_node;
   int depth;
@@ -308,7 +308,7 @@ struct RouteShared {
 
 // Gathers everything the routing reads in one parallel round (the tree, the
 // row statistics, the uniforms and each node's token logit in its parent's
-// row -- the only logits routing touches), then walks on one thread: from v,
+// row -- the only logits routing touches), then walks on one wave: from v,
 // the children in ascending node order accumulate S += E(x_v[token] - m_v) and
 // the first child with u[2d] * Z_v < S is accepted.  Accepted nodes are
 // written to nodes_out when write_nodes.  Ends with a barrier.
@@ -329,26 +329,11 @@ __device__ void route_request(const SgTreeSampleArgs& a, int req, int r0, int n,
   }
   for (int k = tid; k < n_u; k += blockDim.x) sh.u[k] = u[k];
   __syncthreads();
-  // Children in ascending node order as first-child / next-sibling links.
-  for (int k = tid; k < n; k += blockDim.x) {
-    int first = -1;
-    for (int c = k + 1; c < n; ++c)
-      if (sh.parent[c] == k) {
-        first = c;
-        break;
-      }
-    sh.first_child[k] = first;
-    int next = -1;
-    const int p = sh.parent[k];
-    for (int c = k + 1; k > 0 && c < n; ++c)
-      if (sh.parent[c] == p) {
-        next = c;
-        break;
-      }
-    sh.next_sibling[k] = next;
-  }
-  __syncthreads();
-  if (tid == 0) {
+  // Wave 0 walks; every lane holds the same state.  The children of v, in
+  // ascending node order, are the nodes c > v with parent v, found 64 at a
+  // time by ballot and visited lowest bit first.
+  if (tid < kWave) {
+    const int lane = tid;
     int32_t* nodes_out = a.accept_nodes_dev + static_cast<int64_t>(a.max_depth) * req;
     int v = 0;
     int depth = 0;
@@ -362,16 +347,21 @@ __device__ void route_request(const SgTreeSampleArgs& a, int req, int r0, int n,
       const float threshold = sh.u[2 * depth] * sh.rz[v];
       float cumulative = 0.0f;
       int accepted = -1;
-      for (int c = sh.first_child[v]; c >= 0; c = sh.next_sibling[c]) {
-        const int tok = sh.token[c];
-        if (tok < 0 || tok >= a.vocab) {
-          accepted = -2;  // draft token outside the vocabulary
-          break;
-        }
-        cumulative = cumulative + sg_exp(sh.xchild[c] - m);
-        if (threshold < cumulative) {
-          accepted = c;
-          break;
+      for (int base = v + 1; base < n && accepted == -1; base += kWave) {
+        uint64_t mask = __ballot(base + lane < n && sh.parent[base + lane] == v);
+        while (mask != 0) {
+          const int c = base + __builtin_ctzll(mask);
+          mask &= mask - 1;
+          const int tok = sh.token[c];
+          if (tok < 0 || tok >= a.vocab) {
+            accepted = -2;  // draft token outside the vocabulary
+            break;
+          }
+          cumulative = cumulative + sg_exp(sh.xchild[c] - m);
+          if (threshold < cumulative) {
+            accepted = c;
+            break;
+          }
         }
       }
       if (accepted >= 0 && depth >= a.max_depth) accepted = -2;
@@ -380,17 +370,24 @@ __device__ void route_request(const SgTreeSampleArgs& a, int req, int r0, int n,
         break;
       }
       if (accepted < 0) break;
-      if (write_nodes) nodes_out[depth] = accepted;
+      if (write_nodes && lane == 0) nodes_out[depth] = accepted;
       v = accepted;
       ++depth;
     }
     int count = 0;
-    for (int c = sh.first_child[v]; c >= 0; c = sh.next_sibling[c])
-      sh.child_tok[count++] = sh.token[c];
-    sh.child_count = count;
-    sh.exit_node = v;
-    sh.depth = depth;
-    sh.broken = broken;
+    for (int base = v + 1; base < n; base += kWave) {
+      const bool is_child = base + lane < n && sh.parent[base + lane] == v;
+      const uint64_t mask = __ballot(is_child);
+      if (is_child)
+        sh.child_tok[count + __popcll(mask & ((1ull << lane) - 1ull))] = sh.token[base + lane];
+      count += __popcll(mask);
+    }
+    if (lane == 0) {
+      sh.child_count = count;
+      sh.exit_node = v;
+      sh.depth = depth;
+      sh.broken = broken;
+    }
   }
   __syncthreads();
 }
@@ -401,7 +398,8 @@ __device__ void route_request(const SgTreeSampleArgs& a, int req, int r0, int n,
 // total of one slab of the exit row:
 //   e = E(x - m) for non-child tokens below vocab, 0 otherwise; group sums
 //   ((e0+e1)+e2)+e3; inclusive Kogge-Stone scan over the 64 lanes of a line;
-//   slab total = sequential sum of the line totals.
+//   slab total = sequential sum of the line totals.  The line totals are kept
+//   too, for part 2.
 template <bool kVec4>
 __global__ __launch_bounds__(kWalkThreads) void exit_totals_kernel(SgTreeSampleArgs a) {
   __shared__ RouteShared sh;
@@ -454,30 +452,30 @@ __global__ __launch_bounds__(kWalkThreads) void exit_totals_kernel(SgTreeSampleA
   float lp = 0.0f;
 #pragma unroll
   for (int j = 0; j < kLinesPerSlab; ++j) lp = lp + total[j];
-  if (lane == 0)
-    static_cast<float*>(a.workspace_dev)[static_cast<int64_t>(req) * slabs + s] = lp;
+  if (lane == 0) {
+    float* ws = static_cast<float*>(a.workspace_dev);
+    ws[static_cast<int64_t>(req) * slabs + s] = lp;
+    float* lines = ws + static_cast<int64_t>(a.num_requests) * slabs +
+                   (static_cast<int64_t>(req) * slabs + s) * kLinesPerSlab;
+#pragma unroll
+    for (int j = 0; j < kLinesPerSlab; ++j) lines[j] = total[j];
+  }
 }
 
-// Walk, part 2 (one workgroup per request): slab prefixes P_s (sequential),
+// Walk, part 2 (one wave per request): slab prefixes P_s (sequential),
 // C = P_slabs, threshold u[2d+1] * C; the bonus is the first non-child token
 // whose running value (P_s + line prefix + lane prefix + its group's
 // elements) exceeds the threshold; fallback: the largest non-child token.
-// A slab whose P_s + T_s lies below threshold - 1e-4 * C cannot hold that
-// token (its running values differ from P_s + T_s by a few roundings), so
-// the ordered scan starts at the first slab that may.
+// The line prefix is the sequential sum of the slab's earlier line totals,
+// which part 1 stored.  A line whose P_s + line prefix + line total lies below
+// threshold - 1e-4 * C cannot hold that token (its running values differ from
+// that sum by a few roundings), so only the lines from the first one that may
+// are recomputed, one 256-token line at a time.
 template <bool kVec4>
-__global__ __launch_bounds__(kWalkThreads) void exit_find_kernel(SgTreeSampleArgs a) {
+__global__ __launch_bounds__(kWave) void exit_find_kernel(SgTreeSampleArgs a) {
   __shared__ int s_child_tok[kMaxTreeRows];
-  __shared__ int s_wave_count[kWalkWaves];
-  __shared__ float s_slab_prefix[kMaxSlabs + 1];
-  __shared__ float s_total[kMaxSlabs];
-  __shared__ int s_first;
-  __shared__ int s_candidate;
-  __shared__ float s_threshold;
   const int req = blockIdx.x;
-  const int tid = threadIdx.x;
-  const int lane = tid & (kWave - 1);
-  const int wave = tid / kWave;
+  const int lane = threadIdx.x;
   const int r0 = a.row_offset_dev[req];
   const int n = a.row_offset_dev[req + 1] - r0;
   if (n < 1 || n > kMaxTreeRows) return;
@@ -486,84 +484,95 @@ __global__ __launch_bounds__(kWalkThreads) void exit_find_kernel(SgTreeSampleArg
   const int v = depth > 0 ? a.accept_nodes_dev[static_cast<int64_t>(a.max_depth) * req + depth - 1]
                           : 0;
   // Children of the exit node in ascending node order.
-  const bool is_child = tid < n && tid > v && a.parent_dev[r0 + tid] == v;
-  const uint64_t mask = __ballot(is_child);
-  if (lane == 0) s_wave_count[wave] = __popcll(mask);
-  __syncthreads();
-  int offset = 0;
   int count = 0;
-  for (int w = 0; w < kWalkWaves; ++w) {
-    offset += (w < wave) ? s_wave_count[w] : 0;
-    count += s_wave_count[w];
+  for (int base = v + 1; base < n; base += kWave) {
+    const bool is_child = base + lane < n && a.parent_dev[r0 + base + lane] == v;
+    const uint64_t mask = __ballot(is_child);
+    if (is_child)
+      s_child_tok[count + __popcll(mask & ((1ull << lane) - 1ull))] = a.token_dev[r0 + base + lane];
+    count += __popcll(mask);
   }
-  if (is_child) s_child_tok[offset + __popcll(mask & ((1ull << lane) - 1ull))] =
-      a.token_dev[r0 + tid];
   const int slabs = (a.vocab + kSlab - 1) / kSlab;
   const float* __restrict__ totals =
       static_cast<const float*>(a.workspace_dev) + static_cast<int64_t>(req) * slabs;
+  const float* __restrict__ line_totals = static_cast<const float*>(a.workspace_dev) +
+                                          static_cast<int64_t>(a.num_requests) * slabs +
+                                          static_cast<int64_t>(req) * slabs * kLinesPerSlab;
   const float* __restrict__ u = a.uniforms_dev + static_cast<int64_t>(a.uniform_stride) * req;
-  for (int s = tid; s < slabs; s += blockDim.x) s_total[s] = totals[s];
-  __syncthreads();
-  if (tid == 0) {
-    float prefix = 0.0f;
-    for (int s = 0; s < slabs; ++s) {
-      s_slab_prefix[s] = prefix;
-      prefix = prefix + s_total[s];
-    }
-    s_slab_prefix[slabs] = prefix;
-    const float threshold = u[2 * depth + 1] * prefix;
-    const float bound = threshold - 1e-4f * prefix;
-    int first = slabs;
-    for (int s = 0; s < slabs; ++s) {
-      if (s_slab_prefix[s] + s_total[s] > bound) {
-        first = s;
-        break;
-      }
-    }
-    s_first = first;
-    s_threshold = threshold;
-    s_candidate = INT_MAX;
+  // C and the threshold (every lane runs the same sequential sums).
+  float prefix = 0.0f;
+  for (int s = 0; s < slabs; ++s) prefix = prefix + totals[s];
+  const float threshold = u[2 * depth + 1] * prefix;
+  const float bound = threshold - 1e-4f * prefix;
+  // First line that may hold the bonus: slab s, line j, base = P_s + lp_j.
+  int s = 0;
+  float slab_prefix = 0.0f;
+  while (s < slabs && !(slab_prefix + totals[s] > bound)) {
+    slab_prefix = slab_prefix + totals[s];
+    ++s;
   }
-  __syncthreads();
+  int j = 0;
+  float lp = 0.0f;
+  if (s < slabs) {
+    const float* lt = line_totals + static_cast<int64_t>(s) * kLinesPerSlab;
+    while (j < kLinesPerSlab - 1 && !((slab_prefix + lp) + lt[j] > bound)) {
+      lp = lp + lt[j];
+      ++j;
+    }
+  }
   const int64_t row = r0 + v;
   const float* __restrict__ x = a.logits_dev + a.logits_row_stride * row;
   const float m = a.row_max_dev[row];
-  const float threshold = s_threshold;
-  for (int base = s_first; base < slabs; base += kWalkWaves) {
-    const int s = base + wave;
-    if (s < slabs) {
-      float e[32], incl[kLinesPerSlab], total[kLinesPerSlab];
-      const uint32_t bits = child_bits(s_child_tok, count, s, lane);
-      exit_values<kVec4>(x, a.vocab, m, s, lane, bits, e);
-      line_scans(e, lane, incl, total);
-      const float slab_prefix = s_slab_prefix[s];
-      int candidate = INT_MAX;
-      float lp = 0.0f;
+  int candidate = INT_MAX;
+  while (s < slabs && candidate == INT_MAX) {
+    // Line j of slab s: lane l holds tokens 2048*s + 256*j + 4*l + c.
+    const int t0 = s * kSlab + kLine * j + 4 * lane;
+    float e[4];
+    if (kVec4 && t0 + 3 < a.vocab) {
+      const float4 q = *reinterpret_cast<const float4*>(x + t0);
+      e[0] = q.x;
+      e[1] = q.y;
+      e[2] = q.z;
+      e[3] = q.w;
+    } else {
 #pragma unroll
-      for (int j = 0; j < kLinesPerSlab; ++j) {
-        const float up = __shfl_up(incl[j], 1);
-        const float excl = (lane > 0) ? up : 0.0f;
-        float run = (slab_prefix + lp) + excl;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const int t = s * kSlab + kLine * j + 4 * lane + c;
-          run = run + e[4 * j + c];
-          const bool hit = t < a.vocab && !((bits >> (4 * j + c)) & 1u) && run > threshold;
-          candidate = (hit && candidate == INT_MAX) ? t : candidate;
-        }
-        lp = lp + total[j];
-      }
-#pragma unroll
-      for (int d = 32; d >= 1; d >>= 1) candidate = min(candidate, __shfl_xor(candidate, d));
-      if (lane == 0 && candidate != INT_MAX) atomicMin(&s_candidate, candidate);
+      for (int c = 0; c < 4; ++c) e[c] = (t0 + c < a.vocab) ? x[t0 + c] : -__builtin_inff();
     }
-    __syncthreads();
-    const int found = s_candidate;
-    __syncthreads();
-    if (found != INT_MAX) break;
+    const uint32_t bits = child_bits(s_child_tok, count, s, lane) >> (4 * j);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float val = sg_exp_nonpos(e[c] - m);
+      e[c] = ((bits >> c) & 1u) ? 0.0f : val;
+    }
+    // The same group sums and inclusive Kogge-Stone scan as part 1.
+    float g = ((e[0] + e[1]) + e[2]) + e[3];
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const float up = __shfl_up(g, d);
+      g = (lane >= d) ? g + up : g;
+    }
+    const float up = __shfl_up(g, 1);
+    const float excl = (lane > 0) ? up : 0.0f;
+    float run = (slab_prefix + lp) + excl;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      run = run + e[c];
+      const bool hit = t0 + c < a.vocab && !((bits >> c) & 1u) && run > threshold;
+      candidate = (hit && candidate == INT_MAX) ? t0 + c : candidate;
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) candidate = min(candidate, __shfl_xor(candidate, d));
+    // Next line: line prefixes restart at each slab.
+    lp = lp + __shfl(g, kWave - 1);
+    if (++j == kLinesPerSlab) {
+      slab_prefix = slab_prefix + totals[s];
+      lp = 0.0f;
+      j = 0;
+      ++s;
+    }
   }
-  if (tid == 0) {
-    int bonus = s_candidate;
+  if (lane == 0) {
+    int bonus = candidate;
     if (bonus == INT_MAX) {
       bonus = -1;
       for (int t = a.vocab - 1; t >= 0; --t) {
@@ -624,8 +633,9 @@ extern "C" int sg_row_stats(const float* logits_dev, int64_t row_stride, int32_t
 extern "C" int64_t sg_tree_sample_workspace_bytes(int32_t num_requests, int32_t vocab) {
   using namespace sg;
   if (num_requests < 0 || vocab < 1) return 0;
+  // Per request and slab: the slab's complement total and its line totals.
   return static_cast<int64_t>(num_requests) * ((vocab + kSlab - 1) / kSlab) *
-         static_cast<int64_t>(sizeof(float));
+         (1 + kLinesPerSlab) * static_cast<int64_t>(sizeof(float));
 }
 
 extern "C" int sg_tree_sample(const SgTreeSampleArgs* args, sg_stream_t stream) {
@@ -656,12 +666,12 @@ extern "C" int sg_tree_sample(const SgTreeSampleArgs* args, sg_stream_t stream) 
   if (vec4_ok(a.logits_dev, a.logits_row_stride, a.vocab)) {
     hipLaunchKernelGGL(exit_totals_kernel<true>, grid1, dim3(kWalkThreads), 0, s, a);
     SG_LAUNCH_CHECK();
-    hipLaunchKernelGGL(exit_find_kernel<true>, dim3(a.num_requests), dim3(kWalkThreads), 0, s,
+    hipLaunchKernelGGL(exit_find_kernel<true>, dim3(a.num_requests), dim3(kWave), 0, s,
                        a);
   } else {
     hipLaunchKernelGGL(exit_totals_kernel<false>, grid1, dim3(kWalkThreads), 0, s, a);
     SG_LAUNCH_CHECK();
-    hipLaunchKernelGGL(exit_find_kernel<false>, dim3(a.num_requests), dim3(kWalkThreads), 0, s,
+    hipLaunchKernelGGL(exit_find_kernel<false>, dim3(a.num_requests), dim3(kWave), 0, s,
                        a);
   }
   SG_LAUNCH_CHECK();
