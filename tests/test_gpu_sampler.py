@@ -105,6 +105,25 @@ def test_long_context_trees_bit_exact(device, oracle):
     assert gpu["accept_len"].max() >= 3
 
 
+def test_exit_draws_spread_over_the_vocabulary(device, oracle):
+    """Unboosted children: most walks exit at the root, and the 64 residual
+    draws land in lines all over a 151,936-token row (the exit search starts
+    at the first line that may hold the bonus)."""
+    case = tree_problem(21, num_requests=64, nodes=3, vocab=151936, child_boost=0.0)
+    gpu = _check_case(case, device, oracle)
+    assert len(set((gpu["bonus"] // 256).tolist())) > 32  # many distinct lines
+
+
+def test_wide_exit_node(device, oracle):
+    """Roots with 200 children: the children are found by several 64-lane
+    ballots, and 200 tokens are excluded from the residual draw; extreme
+    uniforms included."""
+    trees = [[-1] + [0] * 200 for _ in range(6)]
+    case = tree_problem(22, num_requests=6, nodes=None, vocab=8192, child_boost=0.5,
+                        trees=trees, extreme_uniforms=True)
+    _check_case(case, device, oracle)
+
+
 def test_golden_fixture(device):
     from pathlib import Path
     path = Path(__file__).parent / "golden" / "sampler_tiny.npz"
