@@ -12,8 +12,9 @@
 //   unit      = (request, kv head, tile of up to 128/G query rows = 128 query
 //               vectors = four 32-vector q-groups, range of prefix keys); the
 //               unit that ends a request's key range also covers its tree rows;
-//   work list = the units one workgroup runs in order; the host planner packs
-//               units onto lists (lists c and c + 256 share a CU);
+//   work list = the units one workgroup runs in order; by default one unit,
+//               largest first, so that the hardware dispatcher balances the
+//               end of the launch;
 //   window    = one barrier; consumes one group of 32-key K and V tiles, moved
 //               HBM -> LDS by global_load_lds_dwordx4 (no register staging)
 //               into 4-tile rings issued two to four windows ahead;
@@ -1026,15 +1027,18 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
   std::iota(order.begin(), order.end(), size_t{0});
   std::stable_sort(order.begin(), order.end(),
                    [&](size_t x, size_t y) { return cost[x] > cost[y]; });
-  const int64_t bins = std::min<int64_t>(target, static_cast<int64_t>(units.size()));
-  // Units are first packed onto CUs (pairs of lists c and c + bins/2, which
-  // dispatch order places on one CU: every CU's first slot is filled before
-  // any second slot), then split between the CU's two workgroups.
+  // By default every unit is a work list of its own, in decreasing cost
+  // order.  The first two per CU start at once, the largest on each CU's
+  // first slot (which the CU's issue arbitration favours), and the hardware
+  // dispatcher starts every further unit on the first slot that frees: greedy
+  // list scheduling at the speed each slot actually achieves.  With a target
+  // hint the units are packed onto that many lists instead.
+  const int64_t bins = target_units_hint > 0
+                           ? std::min<int64_t>(target, static_cast<int64_t>(units.size()))
+                           : static_cast<int64_t>(units.size());
   constexpr int64_t kXcds = 8;
-  const bool paired = kListsPerCU == 2 && bins % (2 * kXcds) == 0;
-  const int64_t lpt_bins = paired ? bins / 2 : bins;
-  std::vector<int64_t> load(lpt_bins, 0);
-  std::vector<std::vector<size_t>> bin_units(lpt_bins);
+  std::vector<int64_t> load(bins, 0);
+  std::vector<std::vector<size_t>> bin_units(bins);
   // Units that read the same (request, kv head) K/V (the row tiles of a tree
   // larger than one tile, and split pieces) go to lists of one XCD: the
   // dispatcher places workgroup b on XCD b % 8, whose L2 then serves the
@@ -1043,8 +1047,8 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
   for (size_t k : order) {
     const size_t key = static_cast<size_t>(units[k].req) * num_kv_heads + units[k].kv_head;
     int64_t b = -1;
-    if (xcd_of[key] >= 0 && lpt_bins >= kXcds) {
-      for (int64_t c = xcd_of[key]; c < lpt_bins; c += kXcds)
+    if (xcd_of[key] >= 0 && bins >= kXcds) {
+      for (int64_t c = xcd_of[key]; c < bins; c += kXcds)
         if (b < 0 || load[c] < load[b]) b = c;
     } else {
       b = std::min_element(load.begin(), load.end()) - load.begin();
@@ -1055,7 +1059,7 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
   }
   // Local search: move a unit out of the most loaded list, or swap it with a
   // smaller unit of the least loaded list, while that lowers the maximum.
-  for (int round = 0; lpt_bins > 1 && round < 4096; ++round) {
+  for (int round = 0; bins > 1 && round < 4096; ++round) {
     const int64_t hi = std::max_element(load.begin(), load.end()) - load.begin();
     const int64_t lo = std::min_element(load.begin(), load.end()) - load.begin();
     const int64_t gap = load[hi] - load[lo];
@@ -1080,34 +1084,16 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
     load[hi] -= best;
     load[lo] += best;
   }
-  if (paired) {
-    // The CU's first-dispatched workgroup is older and wins its issue
-    // arbitration: measured on MI355X with equal lists, the second one takes
-    // 1.22x as long.  The first list gets the larger share, 55:45.
-    constexpr int64_t kFirstShare = 55, kSecondShare = 45;
-    std::vector<std::vector<size_t>> lists(bins);
-    for (int64_t c = 0; c < lpt_bins; ++c) {
-      std::vector<size_t>& us = bin_units[c];
-      std::stable_sort(us.begin(), us.end(),
-                       [&](size_t x, size_t y) { return cost[x] > cost[y]; });
-      int64_t l0 = 0, l1 = 0;
-      for (size_t k : us) {
-        if ((l0 + cost[k]) * kSecondShare <= (l1 + cost[k]) * kFirstShare) {
-          lists[c].push_back(k);
-          l0 += cost[k];
-        } else {
-          lists[c + lpt_bins].push_back(k);
-          l1 += cost[k];
-        }
-      }
-    }
-    bin_units = std::move(lists);
-  }
+  // Lists left empty by the XCD placement are dropped.
+  bin_units.erase(std::remove_if(bin_units.begin(), bin_units.end(),
+                                 [](const std::vector<size_t>& b) { return b.empty(); }),
+                  bin_units.end());
+  const int64_t lists = static_cast<int64_t>(bin_units.size());
 
   const size_t bytes = sizeof(PlanHeader) + sizeof(AttnUnit) * units.size() +
-                       sizeof(MergeGroup) * merges.size() + sizeof(int32_t) * (bins + 1);
+                       sizeof(MergeGroup) * merges.size() + sizeof(int32_t) * (lists + 1);
   *plan_bytes = bytes;
-  *plan_units = static_cast<int32_t>(bins);
+  *plan_units = static_cast<int32_t>(lists);
   *plan_merges = static_cast<int32_t>(merges.size());
   *workspace_bytes = sizeof(float) * partial_floats(head_dim) * static_cast<size_t>(partials);
   if (plan_host == nullptr) return SG_OK;  // size query
@@ -1120,18 +1106,18 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
   hdr.head_dim = head_dim;
   hdr.group = G;
   hdr.num_partials = partials;
-  hdr.num_bins = static_cast<int32_t>(bins);
+  hdr.num_bins = static_cast<int32_t>(lists);
   char* out = static_cast<char*>(plan_host);
   std::memcpy(out, &hdr, sizeof(hdr));
   AttnUnit* uo = reinterpret_cast<AttnUnit*>(out + sizeof(hdr));
   MergeGroup* mo = reinterpret_cast<MergeGroup*>(uo + units.size());
   int32_t* bo = reinterpret_cast<int32_t*>(mo + merges.size());
   size_t next = 0;
-  for (int64_t b = 0; b < bins; ++b) {
+  for (int64_t b = 0; b < lists; ++b) {
     bo[b] = static_cast<int32_t>(next);
     for (size_t k : bin_units[b]) uo[next++] = units[k];
   }
-  bo[bins] = static_cast<int32_t>(next);
+  bo[lists] = static_cast<int32_t>(next);
   std::memcpy(mo, merges.data(), sizeof(MergeGroup) * merges.size());
   return SG_OK;
 }

@@ -36,8 +36,10 @@ def _check_plan(wl, target):
                               wl.head_dim, target)
     header, units, merges, bins = ops.decode_plan(plan)
     assert header[0] == 0x53475041 and header[2] == plan.merges
-    # work lists: one per workgroup, contiguous, covering every unit once
-    assert header[7] == plan.units == min(target if target > 0 else 512, len(units))
+    # work lists: one per workgroup, contiguous, non-empty, covering every unit
+    # once; by default one unit per list, else at most `target` lists
+    expected = min(target, len(units)) if target > 0 else len(units)
+    assert header[7] == plan.units and 0 < plan.units <= expected
     assert bins[0] == 0 and bins[-1] == len(units) and (np.diff(bins) >= 1).all()
     rows_per_tile = 128 // (wl.num_q_heads // wl.num_kv_heads)
     cover = {}
