@@ -476,6 +476,7 @@ __global__ __launch_bounds__(kWalkThreads) void exit_totals_kernel(SgTreeSampleA
 template <bool kVec4>
 __global__ __launch_bounds__(kWave) void exit_find_kernel(SgTreeSampleArgs a) {
   __shared__ int s_child_tok[kMaxTreeRows];
+  __shared__ float s_total[kMaxSlabs];
   const int req = blockIdx.x;
   const int lane = threadIdx.x;
   const int r0 = a.row_offset_dev[req];
@@ -501,17 +502,45 @@ __global__ __launch_bounds__(kWave) void exit_find_kernel(SgTreeSampleArgs a) {
                                           static_cast<int64_t>(a.num_requests) * slabs +
                                           static_cast<int64_t>(req) * slabs * kLinesPerSlab;
   const float* __restrict__ u = a.uniforms_dev + static_cast<int64_t>(a.uniform_stride) * req;
+  // The slab totals go to LDS in one parallel round trip; the sequential sums
+  // below then read them in batches of eight, in the same order.
+  for (int k = lane; k < slabs; k += kWave) s_total[k] = totals[k];
+  __builtin_amdgcn_wave_barrier();
   // C and the threshold (every lane runs the same sequential sums).
   float prefix = 0.0f;
-  for (int s = 0; s < slabs; ++s) prefix = prefix + totals[s];
+  {
+    int k = 0;
+    for (; k + 8 <= slabs; k += 8) {
+      float t[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) t[e] = s_total[k + e];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) prefix = prefix + t[e];
+    }
+    for (; k < slabs; ++k) prefix = prefix + s_total[k];
+  }
   const float threshold = u[2 * depth + 1] * prefix;
   const float bound = threshold - 1e-4f * prefix;
   // First line that may hold the bonus: slab s, line j, base = P_s + lp_j.
   int s = 0;
   float slab_prefix = 0.0f;
-  while (s < slabs && !(slab_prefix + totals[s] > bound)) {
-    slab_prefix = slab_prefix + totals[s];
-    ++s;
+  {
+    bool found = false;
+    while (!found && s < slabs) {
+      float t[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) t[e] = s + e < slabs ? s_total[s + e] : 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (found || s >= slabs) continue;
+        if (slab_prefix + t[e] > bound) {
+          found = true;
+        } else {
+          slab_prefix = slab_prefix + t[e];
+          ++s;
+        }
+      }
+    }
   }
   int j = 0;
   float lp = 0.0f;
@@ -567,7 +596,7 @@ __global__ __launch_bounds__(kWave) void exit_find_kernel(SgTreeSampleArgs a) {
     // Next line: line prefixes restart at each slab.
     lp = lp + __shfl(g, kWave - 1);
     if (++j == kLinesPerSlab) {
-      slab_prefix = slab_prefix + totals[s];
+      slab_prefix = slab_prefix + s_total[s];
       lp = 0.0f;
       j = 0;
       ++s;
