@@ -62,7 +62,7 @@ constexpr int32_t kPlanMagic = 0x53475041;  // "SGPA"
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazyLog2 = 8.0f;  // softmax reference point moves after a 2^8 growth
 constexpr int kDefaultCUs = 256;
-constexpr int64_t kSplitAbovePercent = 150;  // planner: split units above 1.5x a mean list
+constexpr int64_t kSplitAbovePercent = 150;  // planner: split units above 1.5x a slot's share
 
 struct PlanHeader {
   int32_t magic;
@@ -791,8 +791,8 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
   }
 }
 
-// One workgroup per work list (one per CU): the units of list b are
-// units[bin_offset[b] .. bin_offset[b+1]), processed in order.
+// One workgroup per work list (two resident per CU): the units of list b
+// are units[bin_offset[b] .. bin_offset[b+1]), processed in order.
 template <int D>
 __global__ __launch_bounds__(kThreads, kListsPerCU) void tree_attn_kernel(SgTreeAttnArgs a) {
   const PlanHeader* hdr = static_cast<const PlanHeader*>(a.plan_dev);
@@ -933,9 +933,10 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
     chunk = per_unit * kTileKeys;
   }
 
-  // Balance: a unit costing more than kSplitAbovePercent % of the mean work
-  // list is split over its prefix into pieces below that bound, so that the
-  // lists can be packed evenly (each split costs a partial write and a merge).
+  // Balance: a unit costing more than kSplitAbovePercent % of a CU slot's
+  // mean share is split over its prefix into pieces below that bound, so that
+  // no unit dominates the end of the launch (each piece costs a prologue, a
+  // partial write and a merge, so the bound is high).
   auto unit_cost = [&](int row_count, int64_t tiles) -> int64_t {
     const int nq = (row_count * G + 31) / 32;
     return nq <= 2 ? 550 + 57 * tiles : 840 + 88 * tiles;
@@ -1009,12 +1010,11 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
       }
     }
   }
-  // Work lists: units are packed onto `target` workgroups (one per CU) by
-  // longest-processing-time-first greedy assignment to the least-loaded list.
-  // Unit cost (hundredths of a microsecond on MI355X at 32q/8kv, D=128): a
-  // fixed part (prologue latency, epilogue) plus a per-64-key-tile part; a
-  // unit with at most two q-groups (64 query vectors) streams two tiles per
-  // window and costs less per tile.
+  // Unit cost, the order of the lists and the packing of a hinted list count
+  // (hundredths of a microsecond on MI355X at 32q/8kv, D=128): a fixed part
+  // (prologue latency, epilogue) plus a part per 32-key tile; a unit with at
+  // most two q-groups (64 query vectors) streams two tiles per window and
+  // costs less per tile.
   std::vector<int64_t> cost(units.size());
   for (size_t k = 0; k < units.size(); ++k) {
     const int rows = row_offset_host[units[k].req + 1] - row_offset_host[units[k].req];
