@@ -63,6 +63,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazyLog2 = 8.0f;  // softmax reference point moves after a 2^8 growth
 constexpr int kDefaultCUs = 256;
 constexpr int64_t kSplitAbovePercent = 150;  // planner: split units above 1.5x a slot's share
+constexpr int64_t kRowSplitAbovePercent = 150;  // planner: units split by rows instead
 
 struct PlanHeader {
   int32_t magic;
@@ -85,7 +86,8 @@ struct AttnUnit {
   int32_t key_begin;
   int32_t key_end;
   int32_t partial;        // partial slot of this unit, -1 when unsplit
-  int32_t flags;          // bit 0: attend to the request's tree rows
+  int32_t flags;          // bit 0: attend to the request's tree rows; bit 1: rows
+                          // split, K/V shared with sibling units (no nt hint)
   int32_t group;          // split group (merge record index), -1 when unsplit
   int32_t num_splits;     // units in the group
   int32_t first_partial;  // partial slot of the group's first unit
@@ -265,8 +267,9 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
   const int64_t row = static_cast<int64_t>(r0) + u.row_begin + r_local;
   const int g = u.kv_head;
   const bool do_tree = (u.flags & 1) != 0;
-  // The request's K/V is read by this unit alone when its rows fit one row tile.
-  const bool stream_kv = n * G <= kQPerUnit;
+  // The request's K/V is read by this unit alone when its rows fit one row
+  // tile and the planner did not split the rows (flags bit 1).
+  const bool stream_kv = (u.flags & 2) == 0 && n * G <= kQPerUnit;
 
   // Ancestor-or-self bitsets of the tile's rows (request-local numbering).
   if (do_tree) {
@@ -942,6 +945,7 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
     return nq <= 2 ? 550 + 57 * tiles : 840 + 88 * tiles;
   };
   std::vector<int> balance_splits(num_requests, 1);
+  std::vector<char> split_rows(num_requests, 0);
   {
     int64_t total_cost = 0;
     std::vector<int64_t> req_cost(num_requests, 0);
@@ -957,8 +961,13 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
     }
     const int64_t lists = std::max<int64_t>(1, std::min(target, base_units));
     const int64_t bound = std::max<int64_t>(1, total_cost * kSplitAbovePercent / (100 * lists));
-    for (int i = 0; i < num_requests; ++i)
+    const int64_t row_bound =
+        std::max<int64_t>(1, total_cost * kRowSplitAbovePercent / (100 * lists));
+    for (int i = 0; i < num_requests; ++i) {
       if (req_cost[i] > bound) balance_splits[i] = static_cast<int>((req_cost[i] + bound - 1) / bound);
+      const int rows = row_offset_host[i + 1] - row_offset_host[i];
+      split_rows[i] = req_cost[i] > row_bound && rows * G > kQPerUnit / 2;
+    }
   }
   std::vector<AttnUnit> units;
   std::vector<MergeGroup> merges;
@@ -967,12 +976,18 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
     const int rows = row_offset_host[i + 1] - row_offset_host[i];
     if (rows == 0) continue;
     const int L = prefix_len_host[i];
+    // A large unit with more than two q-groups is split by rows into units of
+    // 64 query vectors (half a row tile), which read the same K/V on one XCD
+    // (L2 serves the second read) and need no merge; only a unit of at most
+    // 64 query vectors is split over its prefix.
+    const bool row_split = split_rows[i] != 0;
+    const int rpt = row_split ? rows_per_tile / 2 : rows_per_tile;
     // Pieces keep at least four full tiles of prefix.
-    const int splits = std::max(1, std::min(std::max(balance_splits[i],
+    const int splits = std::max(1, std::min(std::max(row_split ? 1 : balance_splits[i],
                                                      static_cast<int>(std::max<int64_t>(
                                                          1, (L + chunk / 2) / chunk))),
                                             L / (4 * kTileKeys)));
-    const int tiles = (rows + rows_per_tile - 1) / rows_per_tile;
+    const int tiles = (rows + rpt - 1) / rpt;
     for (int g = 0; g < num_kv_heads; ++g) {
       for (int tile = 0; tile < tiles; ++tile) {
         const int group = splits > 1 ? static_cast<int>(merges.size()) : -1;
@@ -981,15 +996,15 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
           AttnUnit u;
           u.req = i;
           u.kv_head = g;
-          u.row_begin = tile * rows_per_tile;
-          u.row_count = std::min(rows_per_tile, rows - u.row_begin);
+          u.row_begin = tile * rpt;
+          u.row_count = std::min(rpt, rows - u.row_begin);
           u.key_begin = static_cast<int32_t>(static_cast<int64_t>(L) * s / splits / kTileKeys *
                                              kTileKeys);
           u.key_end = s + 1 == splits ? L
                                       : static_cast<int32_t>(static_cast<int64_t>(L) * (s + 1) /
                                                              splits / kTileKeys * kTileKeys);
           u.partial = splits > 1 ? partials++ : -1;
-          u.flags = (s + 1 == splits) ? 1 : 0;
+          u.flags = ((s + 1 == splits) ? 1 : 0) | (row_split ? 2 : 0);
           u.group = group;
           u.num_splits = splits;
           u.first_partial = splits > 1 ? first : -1;
@@ -1000,8 +1015,8 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
           MergeGroup mg;
           mg.req = i;
           mg.kv_head = g;
-          mg.row_begin = tile * rows_per_tile;
-          mg.row_count = std::min(rows_per_tile, rows - mg.row_begin);
+          mg.row_begin = tile * rpt;
+          mg.row_count = std::min(rpt, rows - mg.row_begin);
           mg.first_partial = first;
           mg.num_partials = splits;
           mg.pad0 = mg.pad1 = 0;

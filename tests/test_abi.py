@@ -43,16 +43,22 @@ def _check_plan(wl, target):
     assert bins[0] == 0 and bins[-1] == len(units) and (np.diff(bins) >= 1).all()
     rows_per_tile = 128 // (wl.num_q_heads // wl.num_kv_heads)
     cover = {}
+    tile_of = {}  # rows per unit of each request: a full row tile, or half a
+                  # tile when the planner split the rows (flags bit 1)
     for (req, g, row_begin, row_count, kb, ke, partial, flags, group, splits, first,
          _) in units.tolist():
-        assert row_begin % rows_per_tile == 0
-        assert row_count == min(rows_per_tile, int(wl.rows[req]) - row_begin)
+        t = rows_per_tile // 2 if flags & 2 else rows_per_tile
+        assert tile_of.setdefault(req, t) == t
+        if flags & 2:  # only units of more than 64 query vectors are split by rows
+            assert int(wl.rows[req]) * 128 // rows_per_tile > 64
+        assert row_begin % t == 0
+        assert row_count == min(t, int(wl.rows[req]) - row_begin)
         cover.setdefault((req, g, row_begin), []).append(
             (kb, ke, partial, flags, group, splits, first))
     groups = {}
     for req in range(wl.num_requests):
         for g in range(wl.num_kv_heads):
-            for row_begin in range(0, int(wl.rows[req]), rows_per_tile):
+            for row_begin in range(0, int(wl.rows[req]), tile_of[req]):
                 parts = sorted(cover.pop((req, g, row_begin)))
                 assert parts[0][0] == 0 and parts[-1][1] == int(wl.prefix_len[req])
                 for a, b in zip(parts, parts[1:]):
@@ -66,7 +72,7 @@ def _check_plan(wl, target):
                     slots = sorted(p[2] for p in parts)
                     assert slots == list(range(parts[0][6], parts[0][6] + len(parts)))
                     groups[parts[0][4]] = (req, g, row_begin,
-                                           min(rows_per_tile, int(wl.rows[req]) - row_begin),
+                                           min(tile_of[req], int(wl.rows[req]) - row_begin),
                                            parts[0][6], len(parts))
     assert not cover
     assert sorted(groups) == list(range(plan.merges))
