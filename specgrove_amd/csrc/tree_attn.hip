@@ -200,9 +200,6 @@ __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast
 
 __device__ __forceinline__ uint4 zero4() { return make_uint4(0u, 0u, 0u, 0u); }
 
-enum class Mask { kFull, kLimit, kTree };
-template <Mask M>
-using MaskTag = std::integral_constant<Mask, M>;
 template <int N>
 using IntTag = std::integral_constant<int, N>;
 template <bool B>
