@@ -91,11 +91,12 @@ typedef struct SgTreeAttnArgs {
 /* Host-side planner.  From host copies of row_offset [n+1] and prefix_len [n]
  * it writes the work list (plan_capacity_bytes of host memory) and reports its
  * size, its number of work lists (*plan_units: workgroups of the attention
- * kernel, at most target_units_hint or 256, each a list of units packed by
- * estimated cost), its split-merge groups and the scratch bytes
- * sg_tree_attn_fwd needs.  Replaces the
- * host index lists the reference builds per wave (CTBD:327-350, :513-545).
- * target_units_hint <= 0 sizes the work lists and splits for 256 CUs. */
+ * kernel), its split-merge groups and the scratch bytes sg_tree_attn_fwd
+ * needs.  Replaces the host index lists the reference builds per wave
+ * (CTBD:327-350, :513-545).
+ * target_units_hint <= 0: one unit per work list, in decreasing cost order,
+ * with splits sized for 256 CUs; > 0: units packed onto at most that many
+ * lists by estimated cost. */
 int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset_host,
                       const int32_t* prefix_len_host, int32_t num_q_heads,
                       int32_t num_kv_heads, int32_t head_dim,
