@@ -151,3 +151,56 @@ def test_long_prefix_and_single_row_requests(device, oracle):
     for i, ref in refs.items():
         r0, r1 = int(sub.row_offset[i]), int(sub.row_offset[i + 1])
         _assert_close(got[r0:r1], ref)
+
+
+def _tree_of_form(form, rows, rng):
+    if rows == 0:
+        return []
+    if form == "chain":
+        return [-1] + list(range(rows - 1))
+    if form == "star":
+        return [-1] + [0] * (rows - 1)
+    if form == "binary":
+        return [-1] + [(k - 1) // 2 for k in range(1, rows)]
+    return [-1] + [int(rng.integers(0, k)) for k in range(1, rows)]
+
+
+@pytest.mark.parametrize("hq,hkv,dim,seed,q_scale", [
+    (8, 8, 128, 0, None), (16, 2, 64, 1, None), (32, 2, 128, 2, 3.0),
+    (4, 1, 64, 3, 3.0), (32, 8, 128, 4, None), (64, 8, 64, 5, 3.0)])
+def test_random_head_groups_prefixes_and_tree_forms(device, oracle, hq, hkv, dim, seed,
+                                                    q_scale):
+    """Head groups 1-16, head dims 64 and 128, prefixes of 0 to 2049 keys around
+    the 32-key tile edges, chains, stars, binary and random trees from 1 to the
+    256-row maximum, and an empty request.  Few units per wave, so the planner
+    also splits prefixes (partials and the merge kernel).  Sharp scores
+    (q_scale 3) make the running maximum jump, which forces the deferred
+    softmax rescale."""
+    rng = np.random.default_rng(100 + seed)
+    n = 9
+    prefix = rng.choice([0, 1, 31, 32, 33, 65, 127, 500, 2049], n).astype(np.int32)
+    sizes = [int(x) for x in rng.choice([1, 2, 17, 33, 64, 129, 256], n)]
+    sizes[seed % n] = 0
+    forms = ["chain", "star", "binary", "random"]
+    parents = [_tree_of_form(forms[i % 4], sizes[i], rng) for i in range(n)]
+    tokens = [W.random_tokens(p, 4096, rng) for p in parents]
+    capacity = (int(prefix.max()) + 256 + 63) // 64 * 64
+    wl = W.AttentionWorkload(f"random_{seed}", hq, hkv, dim, prefix, parents, tokens,
+                             capacity)
+    tensors = wl.make_tensors("cpu", seed, q_scale=q_scale)
+    dev = [t.to(device) for t in tensors]
+    meta = dict(
+        row_offset=torch.from_numpy(wl.row_offset).to(device),
+        prefix_start=torch.from_numpy(wl.prefix_start).to(device),
+        prefix_len=torch.from_numpy(wl.prefix_len.astype(np.int32)).to(device),
+        parent=torch.from_numpy(wl.parent_flat).to(device),
+    )
+    got, plan = _run(wl, dev, meta, device)
+    ks, vs = _prefix_lists(wl, tensors)
+    q, kc, vc, kt, vt = tensors
+    live = [i for i in range(n) if sizes[i] > 0]
+    refs = oracle.attention_per_request(q, ks, vs, kt, vt, wl.row_offset, wl.parents,
+                                        requests=live)
+    for i in live:
+        r0, r1 = int(wl.row_offset[i]), int(wl.row_offset[i + 1])
+        _assert_close(got[r0:r1], refs[i])
