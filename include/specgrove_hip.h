@@ -117,7 +117,9 @@ int sg_tree_attn_fwd(const SgTreeAttnArgs* args, sg_stream_t stream);
  * for every layer l, kv head g and t < keep_len_i.  If len_i + keep_len_i
  * exceeds capacity the request is not written and *status_dev is set to
  * SG_ERANGE (the reference raises "Persistent request KV capacity exhausted",
- * CTBD:235-236); callers check capacity on the host first.
+ * CTBD:235-236); callers check capacity on the host first.  A kept row
+ * outside [0, row_offset_{i+1} - row_offset_i) likewise leaves the request
+ * unwritten and sets *status_dev to SG_EINVAL.
  * ---------------------------------------------------------------------- */
 typedef struct SgKvCommitArgs {
   int32_t num_layers;

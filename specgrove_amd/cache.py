@@ -136,7 +136,7 @@ class PersistentRequestCachePool:
                                packed_old_length: int, query_offsets: Sequence[int],
                                keep_query_rows: Sequence[Sequence[int]], device) -> None:
         """Scatter only newly accepted query KV rows back to the arena
-        (reference :215-261), all layers in one launch.
+        (reference :215-261), all layers in one sg_kv_commit call.
 
         ``packed`` is the wave's TreeVerifyCache: its layer l holds the new
         rows' K/V [1, Hkv, R, D], so the source row of request i's kept local

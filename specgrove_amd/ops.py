@@ -206,7 +206,7 @@ def kv_commit(k_cache_ptrs: torch.Tensor, v_cache_ptrs: torch.Tensor,
               row_offset: torch.Tensor, keep_rows: torch.Tensor, keep_len: torch.Tensor,
               prefix_start: torch.Tensor, lengths: torch.Tensor, capacity: int,
               status: torch.Tensor | None = None) -> None:
-    """Scatter the kept rows of every layer into the cache (one launch).
+    """Scatter the kept rows of every layer into the cache (one call).
 
     ``*_ptrs`` are int64 device arrays of per-layer base addresses (see
     pointer_array); keep_rows [n, keep_stride] i32, keep_len [n] i32,

@@ -111,3 +111,76 @@ def test_commit_capacity_overflow_reports_erange(device, oracle):
                          np.zeros((1, hkv, n * wl.capacity, d)), lengths.copy(),
                          wl.capacity, range(n), np.zeros((1, wl.total_rows, hkv, d)),
                          np.zeros((1, wl.total_rows, hkv, d)), wl.row_offset, wl.keep)
+
+
+def _raw_commit(device, layers, rows, keep_lists, lengths, capacity, hkv, d, seed):
+    """Commit through the C ABI on random data; returns device and host copies."""
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    n = len(rows)
+    row_offset = np.concatenate([[0], np.cumsum(rows)]).astype(np.int32)
+    cache_k = torch.randn((layers, hkv, n * capacity, d), generator=gen).to(torch.bfloat16)
+    cache_v = torch.randn((layers, hkv, n * capacity, d), generator=gen).to(torch.bfloat16)
+    tree_k = torch.randn((layers, int(row_offset[-1]), hkv, d), generator=gen).to(torch.bfloat16)
+    tree_v = torch.randn((layers, int(row_offset[-1]), hkv, d), generator=gen).to(torch.bfloat16)
+    keep_stride = max(len(k) for k in keep_lists)
+    keep = np.full((n, keep_stride), -1, np.int32)
+    for i, k in enumerate(keep_lists):
+        keep[i, :len(k)] = k
+    dk, dv = cache_k.to(device), cache_v.to(device)
+    tk, tv = tree_k.to(device), tree_v.to(device)
+    lengths_dev = torch.from_numpy(np.asarray(lengths, np.int32)).to(device)
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    ops.kv_commit(
+        ops.pointer_array([dk[l] for l in range(layers)], device),
+        ops.pointer_array([dv[l] for l in range(layers)], device),
+        ops.pointer_array([tk[l] for l in range(layers)], device),
+        ops.pointer_array([tv[l] for l in range(layers)], device),
+        num_kv_heads=hkv, head_dim=d, cache_head_stride=dk.stride(1),
+        cache_token_stride=dk.stride(2), tree_row_stride=tk.stride(1),
+        tree_head_stride=tk.stride(2), row_offset=torch.from_numpy(row_offset).to(device),
+        keep_rows=torch.from_numpy(keep).to(device),
+        keep_len=torch.from_numpy(np.asarray([len(k) for k in keep_lists], np.int32)).to(device),
+        prefix_start=torch.from_numpy(np.arange(n, dtype=np.int64) * capacity).to(device),
+        lengths=lengths_dev, capacity=capacity, status=status)
+    torch.cuda.synchronize()
+    return (dk, dv, lengths_dev, status, cache_k.view(torch.int16).numpy().copy(),
+            cache_v.view(torch.int16).numpy().copy(), tree_k.view(torch.int16).numpy(),
+            tree_v.view(torch.int16).numpy(), row_offset)
+
+
+def test_commit_more_layers_and_kept_rows_than_staged(device, oracle):
+    """130 layers (layer bases beyond the 128 staged in LDS) and a 300-row
+    keep list (kept rows beyond the 256 staged) take the global-memory paths."""
+    rng = np.random.default_rng(7)
+    rows = [320, 5, 40]
+    keep_lists = [[0] + sorted(rng.choice(np.arange(1, 320), 299, replace=False).tolist()),
+                  [0, 3], [0, 1, 7, 30]]
+    lengths = [10, 0, 33]
+    capacity = 400
+    dk, dv, lengths_dev, status, ok, ov, tk, tv, row_offset = _raw_commit(
+        device, 130, rows, keep_lists, lengths, capacity, 1, 8, 11)
+    olen = np.asarray(lengths, np.int32)
+    oracle.kv_commit(ok, ov, olen, capacity, range(3), tk, tv, row_offset, keep_lists)
+    assert int(status.item()) == 0
+    np.testing.assert_array_equal(lengths_dev.cpu().numpy(), olen)
+    assert np.array_equal(dk.cpu().view(torch.int16).numpy(), ok)
+    assert np.array_equal(dv.cpu().view(torch.int16).numpy(), ov)
+
+
+def test_commit_kept_row_outside_the_request_reports_einval(device, oracle):
+    """A kept row past the request's packed rows leaves that request untouched
+    (cache and length) and sets status to SG_EINVAL; the others commit."""
+    rows = [16, 16, 16]
+    keep_lists = [[0, 2, 5], [0, 16], [0, 1]]   # request 1: row 16 of 16 is out of range
+    lengths = [4, 4, 4]
+    capacity = 64
+    dk, dv, lengths_dev, status, ok, ov, tk, tv, row_offset = _raw_commit(
+        device, 2, rows, keep_lists, lengths, capacity, 2, 64, 12)
+    olen = np.asarray(lengths, np.int32)
+    # the oracle commits requests 0 and 2 only
+    oracle.kv_commit(ok, ov, olen, capacity, range(3), tk, tv, row_offset,
+                     [keep_lists[0], [], keep_lists[2]])
+    assert int(status.item()) == -1
+    np.testing.assert_array_equal(lengths_dev.cpu().numpy(), olen)
+    assert np.array_equal(dk.cpu().view(torch.int16).numpy(), ok)
+    assert np.array_equal(dv.cpu().view(torch.int16).numpy(), ov)
