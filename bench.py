@@ -120,6 +120,44 @@ def commit_call(ops, wl, meta, st):
                   lengths=st["lengths"], capacity=wl.capacity)
 
 
+def commit_all_layers(torch, np, ops, wl, meta, device, layers=36, iters=50, warmup=5):
+    """The KV commit of a whole 36-layer Qwen3-8B stack in one call, on
+    distinct per-layer arenas and tree-row staging.  Every call appends the
+    wave's kept rows behind the previous call's, so the calls run back to back
+    (the GPU time per call, not the host's launch time, sets the figure)."""
+    n, hkv, d = wl.num_requests, wl.num_kv_heads, wl.head_dim
+    cap = ((iters + warmup) * max(len(k) for k in wl.keep) + 63) // 64 * 64
+    arena_k = torch.zeros((layers, hkv, n * cap, d), dtype=torch.bfloat16, device=device)
+    arena_v = torch.zeros_like(arena_k)
+    tree_k = torch.randn((layers, wl.total_rows, hkv, d), device=device).to(torch.bfloat16)
+    tree_v = torch.randn_like(tree_k)
+    ptrs = [ops.pointer_array([t[l] for l in range(layers)], device)
+            for t in (arena_k, arena_v, tree_k, tree_v)]
+    start = torch.from_numpy(np.arange(n, dtype=np.int64) * cap).to(device)
+    lengths = torch.zeros(n, dtype=torch.int32, device=device)
+
+    def call(_):
+        ops.kv_commit(*ptrs, num_kv_heads=hkv, head_dim=d,
+                      cache_head_stride=arena_k.stride(1), cache_token_stride=arena_k.stride(2),
+                      tree_row_stride=tree_k.stride(1), tree_head_stride=tree_k.stride(2),
+                      row_offset=meta["row_offset"], keep_rows=meta["keep_rows"],
+                      keep_len=meta["keep_len"], prefix_start=start, lengths=lengths,
+                      capacity=cap)
+    for k in range(warmup):
+        call(k)
+    torch.cuda.synchronize()
+    st, en = _events(torch, 2)
+    st.record()
+    for k in range(iters):
+        call(k)
+    en.record()
+    torch.cuda.synchronize()
+    us = st.elapsed_time(en) / iters * 1e3
+    rows = int(sum(len(k) for k in wl.keep))
+    del arena_k, arena_v, tree_k, tree_v
+    return {"layers": layers, "us_per_call": us, "rows_per_layer": rows,
+            "gbs": 2 * rows * hkv * d * 2 * 2 * layers / (us * 1e-6) / 1e9}
+
 def sampler_bench(torch, W, ops, device, iters, warmup):
     sets = []
     for s in range(N_SETS):
@@ -397,6 +435,7 @@ def main():
             "us_avg": commit_avg * 1e3,
             "rows": int(sum(len(k) for k in wl.keep)),
             "gbs": wl.commit_bytes() / (commit_avg * 1e-3) / 1e9,
+            "all_layers": commit_all_layers(torch, np, ops, wl, meta, device),
         },
     }
 
