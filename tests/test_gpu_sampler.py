@@ -156,3 +156,31 @@ def test_invalid_arguments_raise(device):
         ops.tree_sample(logits, ro, par, tok, u, max_depth=2)
     with pytest.raises(ValueError):
         ops.tree_sample(logits.double(), ro, par, tok, torch.zeros((1, 6), device=device), 2)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_trees_vocabularies_and_acceptance_rates(device, oracle, seed):
+    """Random request counts, tree sizes (a lone root to 200 nodes), chains up
+    to depth 40, vocabularies around the 4-token, 256-token line and
+    2048-token slab edges, child boosts from none (most walks exit at the
+    root) to strong (long accepted paths), and extreme uniforms on some
+    seeds: bit-exact against the oracle."""
+    rng = np.random.default_rng(1000 + seed)
+    vocab = int(rng.choice([5, 255, 257, 2047, 2049, 6143, 32003, 151936]))
+    n = int(rng.integers(1, 13))
+    trees = []
+    for _ in range(n):
+        form = rng.integers(0, 3)
+        size = int(rng.choice([1, 2, 9, 33, 80, 200]))
+        if form == 0:
+            trees.append(W.random_parent_tree(size, rng, max_depth=int(rng.integers(1, 12))))
+        elif form == 1:
+            depth = min(size, 41)
+            trees.append([-1] + list(range(depth - 1)))
+        else:
+            trees.append(W.canonical_tree(size, rng))
+    case = tree_problem(2000 + seed, n, None, vocab, trees=trees,
+                        child_boost=float(rng.choice([0.0, 3.0, 8.0, 14.0])),
+                        logit_std=float(rng.choice([0.5, 3.0, 6.0])),
+                        extreme_uniforms=bool(seed % 3 == 0))
+    _check_case(case, device, oracle)
