@@ -179,7 +179,8 @@ typedef struct SgTreeSampleArgs {
   int32_t* keep_rows_dev;        /* optional [n, max_depth+1]: [0] + nodes, -1 padded */
   int32_t* status_dev;           /* optional [1]: SG_EINVAL if a walk broke the contract */
   void* workspace_dev;           /* >= sg_tree_sample_workspace_bytes(): per-slab
-                                    and per-line complement totals of the exit rows */
+                                    and per-line complement totals of the exit rows,
+                                    and each request's exit node and its children */
   size_t workspace_bytes;
 } SgTreeSampleArgs;
 
@@ -187,7 +188,8 @@ typedef struct SgTreeSampleArgs {
 int sg_tree_sample(const SgTreeSampleArgs* args, sg_stream_t stream);
 
 /* Scratch bytes sg_tree_sample needs for num_requests requests over vocab
- * (4 bytes per 2048-token slab per request).  No reference counterpart. */
+ * (36 bytes per 2048-token slab per request, plus 4,112 bytes per request).
+ * No reference counterpart. */
 int64_t sg_tree_sample_workspace_bytes(int32_t num_requests, int32_t vocab);
 
 /* Row statistics only (max and sum of exp of each logits row). */

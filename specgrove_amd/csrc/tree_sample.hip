@@ -40,6 +40,10 @@ constexpr int kStatsThreads = 512;
 constexpr int kWalkThreads = 1024;
 constexpr int kWalkWaves = kWalkThreads / kWave;
 constexpr int kMaxTreeRows = 1024;
+// Per-request record that the walk's part 1 leaves for part 2 in the
+// workspace, after the slab and line totals: accept length (-1 for a broken
+// walk), exit node, child count, pad, then the exit node's child tokens.
+constexpr int kRecordInts = 4 + kMaxTreeRows;
 
 #define SG_LOG2E 0x1.715476p+0f
 #define SG_LN2_HI 0x1.62e4p-1f
@@ -441,6 +445,18 @@ __global__ __launch_bounds__(kWalkThreads) void exit_totals_kernel(SgTreeSampleA
       for (int k = tid; k <= a.max_depth; k += blockDim.x)
         keep[k] = (k == 0) ? 0 : (!sh.broken && k <= sh.depth ? nodes_out[k - 1] : -1);
     }
+    const int slabs_all = (a.vocab + kSlab - 1) / kSlab;
+    int32_t* rec = reinterpret_cast<int32_t*>(static_cast<float*>(a.workspace_dev) +
+                                              static_cast<int64_t>(a.num_requests) * slabs_all *
+                                                  (1 + kLinesPerSlab)) +
+                   static_cast<int64_t>(req) * kRecordInts;
+    if (tid == 0) {
+      rec[0] = sh.broken ? -1 : sh.depth;
+      rec[1] = sh.exit_node;
+      rec[2] = sh.child_count;
+      rec[3] = 0;
+    }
+    for (int k = tid; k < sh.child_count; k += blockDim.x) rec[4 + k] = sh.child_tok[k];
   }
   if (sh.broken) return;
   const int slabs = (a.vocab + kSlab - 1) / kSlab;
@@ -481,32 +497,42 @@ __global__ __launch_bounds__(kWave) void exit_find_kernel(SgTreeSampleArgs a) {
   __shared__ float s_total[kMaxSlabs];
   const int req = blockIdx.x;
   const int lane = threadIdx.x;
-  const int r0 = a.row_offset_dev[req];
-  const int n = a.row_offset_dev[req + 1] - r0;
-  if (n < 1 || n > kMaxTreeRows) return;
-  const int depth = a.accept_len_dev[req];
-  if (depth < 0) return;  // broken walk, reported by part 1
-  const int v = depth > 0 ? a.accept_nodes_dev[static_cast<int64_t>(a.max_depth) * req + depth - 1]
-                          : 0;
-  // Children of the exit node in ascending node order.
-  int count = 0;
-  for (int base = v + 1; base < n; base += kWave) {
-    const bool is_child = base + lane < n && a.parent_dev[r0 + base + lane] == v;
-    const uint64_t mask = __ballot(is_child);
-    if (is_child)
-      s_child_tok[count + __popcll(mask & ((1ull << lane) - 1ull))] = a.token_dev[r0 + base + lane];
-    count += __popcll(mask);
-  }
   const int slabs = (a.vocab + kSlab - 1) / kSlab;
   const float* __restrict__ totals =
       static_cast<const float*>(a.workspace_dev) + static_cast<int64_t>(req) * slabs;
   const float* __restrict__ line_totals = static_cast<const float*>(a.workspace_dev) +
                                           static_cast<int64_t>(a.num_requests) * slabs +
                                           static_cast<int64_t>(req) * slabs * kLinesPerSlab;
+  const int32_t* rec = reinterpret_cast<const int32_t*>(
+                           static_cast<const float*>(a.workspace_dev) +
+                           static_cast<int64_t>(a.num_requests) * slabs * (1 + kLinesPerSlab)) +
+                       static_cast<int64_t>(req) * kRecordInts;
   const float* __restrict__ u = a.uniforms_dev + static_cast<int64_t>(a.uniform_stride) * req;
-  // The slab totals go to LDS in one parallel round trip; the sequential sums
-  // below then read them in batches of eight, in the same order.
-  for (int k = lane; k < slabs; k += kWave) s_total[k] = totals[k];
+  // One round trip: the row range, part 1's record (accept length, exit node,
+  // child count), the first 64 child tokens and the slab totals.
+  const int r0 = a.row_offset_dev[req];
+  const int n = a.row_offset_dev[req + 1] - r0;
+  const int depth = rec[0];
+  const int v = rec[1];
+  const int count = rec[2];
+  const int tok0 = rec[4 + lane];
+  float tot[(kMaxSlabs + kWave - 1) / kWave];
+#pragma unroll
+  for (int q = 0; q < (kMaxSlabs + kWave - 1) / kWave; ++q)
+    tot[q] = q * kWave + lane < slabs ? totals[q * kWave + lane] : 0.0f;
+  // The record exists only for a valid tree; part 1 reported the others.
+  if (n < 1 || n > kMaxTreeRows) return;
+  if (depth < 0) return;  // broken walk, reported by part 1
+  if (lane < count) s_child_tok[lane] = tok0;
+  for (int k = kWave + lane; k < count; k += kWave) s_child_tok[k] = rec[4 + k];
+#pragma unroll
+  for (int q = 0; q < (kMaxSlabs + kWave - 1) / kWave; ++q)
+    if (q * kWave + lane < slabs) s_total[q * kWave + lane] = tot[q];
+  // The exit draw's uniform and the exit row's max, in flight during the
+  // sums below.
+  const float u_exit = u[2 * depth + 1];
+  const int64_t row = static_cast<int64_t>(r0) + v;
+  const float m = a.row_max_dev[row];
   __builtin_amdgcn_wave_barrier();
   // C and the threshold (every lane runs the same sequential sums).
   float prefix = 0.0f;
@@ -521,7 +547,7 @@ __global__ __launch_bounds__(kWave) void exit_find_kernel(SgTreeSampleArgs a) {
     }
     for (; k < slabs; ++k) prefix = prefix + s_total[k];
   }
-  const float threshold = u[2 * depth + 1] * prefix;
+  const float threshold = u_exit * prefix;
   const float bound = threshold - 1e-4f * prefix;
   // First line that may hold the bonus: slab s, line j, base = P_s + lp_j.
   int s = 0;
@@ -553,9 +579,7 @@ __global__ __launch_bounds__(kWave) void exit_find_kernel(SgTreeSampleArgs a) {
       ++j;
     }
   }
-  const int64_t row = r0 + v;
   const float* __restrict__ x = a.logits_dev + a.logits_row_stride * row;
-  const float m = a.row_max_dev[row];
   int candidate = INT_MAX;
   while (s < slabs && candidate == INT_MAX) {
     // Line j of slab s: lane l holds tokens 2048*s + 256*j + 4*l + c.
@@ -666,9 +690,11 @@ extern "C" int sg_row_stats(const float* logits_dev, int64_t row_stride, int32_t
 extern "C" int64_t sg_tree_sample_workspace_bytes(int32_t num_requests, int32_t vocab) {
   using namespace sg;
   if (num_requests < 0 || vocab < 1) return 0;
-  // Per request and slab: the slab's complement total and its line totals.
-  return static_cast<int64_t>(num_requests) * ((vocab + kSlab - 1) / kSlab) *
-         (1 + kLinesPerSlab) * static_cast<int64_t>(sizeof(float));
+  // Per request and slab: the slab's complement total and its line totals;
+  // then per request the record part 1 leaves for part 2.
+  return static_cast<int64_t>(num_requests) *
+         (((vocab + kSlab - 1) / kSlab) * (1 + kLinesPerSlab) + kRecordInts) *
+         static_cast<int64_t>(sizeof(float));
 }
 
 extern "C" int sg_tree_sample(const SgTreeSampleArgs* args, sg_stream_t stream) {
