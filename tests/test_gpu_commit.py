@@ -184,3 +184,22 @@ def test_commit_kept_row_outside_the_request_reports_einval(device, oracle):
     np.testing.assert_array_equal(lengths_dev.cpu().numpy(), olen)
     assert np.array_equal(dk.cpu().view(torch.int16).numpy(), ok)
     assert np.array_equal(dv.cpu().view(torch.int16).numpy(), ov)
+
+
+def test_commit_overflow_with_several_layers_reports_erange(device, oracle):
+    """Several layers (copy launch + length launch): the request that would
+    pass its capacity is left untouched in every layer and keeps its length;
+    the others commit; status is SG_ERANGE."""
+    rows = [8, 8, 8]
+    keep_lists = [[0, 3], [0, 1], [0, 2, 5]]
+    capacity = 32
+    lengths = [4, capacity - 1, 20]
+    dk, dv, lengths_dev, status, ok, ov, tk, tv, row_offset = _raw_commit(
+        device, 3, rows, keep_lists, lengths, capacity, 2, 64, 13)
+    olen = np.asarray(lengths, np.int32)
+    oracle.kv_commit(ok, ov, olen, capacity, range(3), tk, tv, row_offset,
+                     [keep_lists[0], [], keep_lists[2]])
+    assert int(status.item()) == -2
+    np.testing.assert_array_equal(lengths_dev.cpu().numpy(), olen)
+    assert np.array_equal(dk.cpu().view(torch.int16).numpy(), ok)
+    assert np.array_equal(dv.cpu().view(torch.int16).numpy(), ov)
