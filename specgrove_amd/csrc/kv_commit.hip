@@ -29,10 +29,9 @@ constexpr int kStagedRows = 256;     // kept rows staged in LDS (longer keep lis
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 using GlobalU4 = __attribute__((address_space(1))) u32x4;
 
-// Status of request `req`: SG_OK, SG_ERANGE (its rows would pass the
-// capacity) or SG_EINVAL (a kept row outside its packed rows).  Every
-// workgroup of the request evaluates it on the same inputs, so all of them
-// skip the request or all of them copy it.
+// A request's commit metadata.  Every workgroup of the request checks it on
+// the same inputs (capacity: SG_ERANGE; kept rows inside the request's packed
+// rows: SG_EINVAL), so all of them skip the request or all of them copy it.
 struct CommitRequest {
   int keep_len;
   int len;
@@ -132,6 +131,7 @@ __global__ __launch_bounds__(kCommitThreads) void kv_commit_kernel(SgKvCommitArg
   };
   // Each pass loads four chunks per thread, then stores them: one memory
   // round trip per pass.
+  static_assert(kCommitBatch == 4, "the pass below is written out for four chunks");
   auto copy = [&](auto staged) {
     for (int base = threadIdx.x; base < total; base += kCommitBatch * kCommitThreads) {
       const GlobalU4 *f0, *f1, *f2, *f3;
