@@ -3,6 +3,8 @@
 Tolerance (bf16 inputs and output): max |gpu - ref| <= 2e-2 and
 mean |gpu - ref| / mean |ref| <= 1e-2.
 """
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -165,9 +167,22 @@ def _tree_of_form(form, rows, rng):
     return [-1] + [int(rng.integers(0, k)) for k in range(1, rows)]
 
 
+def _more_random_cases(count):
+    """SG_RANDOM_CASES=N adds N seeded cases to the random test (a longer sweep)."""
+    heads = [(8, 8), (16, 2), (32, 2), (4, 1), (32, 8), (64, 8), (32, 4), (16, 16), (128, 8)]
+    rng = np.random.default_rng(77)
+    cases = []
+    for k in range(count):
+        hq, hkv = heads[int(rng.integers(len(heads)))]
+        cases.append((hq, hkv, int(rng.choice([64, 128])), 100 + k,
+                      [None, 3.0][int(rng.integers(2))]))
+    return cases
+
+
 @pytest.mark.parametrize("hq,hkv,dim,seed,q_scale", [
     (8, 8, 128, 0, None), (16, 2, 64, 1, None), (32, 2, 128, 2, 3.0),
-    (4, 1, 64, 3, 3.0), (32, 8, 128, 4, None), (64, 8, 64, 5, 3.0)])
+    (4, 1, 64, 3, 3.0), (32, 8, 128, 4, None), (64, 8, 64, 5, 3.0)]
+    + _more_random_cases(int(os.environ.get("SG_RANDOM_CASES", "0"))))
 def test_random_head_groups_prefixes_and_tree_forms(device, oracle, hq, hkv, dim, seed,
                                                     q_scale):
     """Head groups 1-16, head dims 64 and 128, prefixes of 0 to 2049 keys around

@@ -1,4 +1,6 @@
 """GPU parity of the tree sampler against the CPU oracle: bit-exact."""
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -158,13 +160,13 @@ def test_invalid_arguments_raise(device):
         ops.tree_sample(logits.double(), ro, par, tok, torch.zeros((1, 6), device=device), 2)
 
 
-@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("seed", range(8 + int(os.environ.get("SG_RANDOM_CASES", "0"))))
 def test_random_trees_vocabularies_and_acceptance_rates(device, oracle, seed):
     """Random request counts, tree sizes (a lone root to 200 nodes), chains up
     to depth 40, vocabularies around the 4-token, 256-token line and
     2048-token slab edges, child boosts from none (most walks exit at the
     root) to strong (long accepted paths), and extreme uniforms on some
-    seeds: bit-exact against the oracle."""
+    seeds: bit-exact against the oracle.  SG_RANDOM_CASES=N adds N seeds."""
     rng = np.random.default_rng(1000 + seed)
     vocab = int(rng.choice([5, 255, 257, 2047, 2049, 6143, 32003, 151936]))
     n = int(rng.integers(1, 13))
@@ -179,6 +181,11 @@ def test_random_trees_vocabularies_and_acceptance_rates(device, oracle, seed):
             trees.append([-1] + list(range(depth - 1)))
         else:
             trees.append(W.canonical_tree(size, rng))
+    # child tokens are distinct per parent, so no parent may have more
+    # children than the vocabulary has tokens
+    widest = max(max(np.bincount(np.asarray(p[1:]), minlength=1)) if len(p) > 1 else 0
+                 for p in trees)
+    vocab = max(vocab, int(widest))
     case = tree_problem(2000 + seed, n, None, vocab, trees=trees,
                         child_boost=float(rng.choice([0.0, 3.0, 8.0, 14.0])),
                         logit_std=float(rng.choice([0.5, 3.0, 6.0])),
