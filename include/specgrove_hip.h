@@ -192,6 +192,21 @@ int sg_tree_sample(const SgTreeSampleArgs* args, sg_stream_t stream);
  * No reference counterpart. */
 int64_t sg_tree_sample_workspace_bytes(int32_t num_requests, int32_t vocab);
 
+/* Size of the static per-GPU scratch of sg_tree_sample_noalloc (4 MiB: e.g.
+ * 615 requests at vocab 151,936). */
+#define SG_TREE_SAMPLE_NOALLOC_SCRATCH_BYTES (4u << 20)
+
+/* sg_tree_sample without any device allocation: the workspace is a static
+ * device array of SG_TREE_SAMPLE_NOALLOC_SCRATCH_BYTES per GPU, held until the
+ * process ends.  args->workspace_dev must be NULL and workspace_bytes 0; calls
+ * whose sg_tree_sample_workspace_bytes() exceeds the maximum return SG_EINVAL.
+ * The caller still passes every input and output.  Calls that overlap on one
+ * GPU (several streams or threads) race on the shared scratch.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). */
+int sg_tree_sample_noalloc(const SgTreeSampleArgs* args, sg_stream_t stream);
+
 /* Row statistics only (max and sum of exp of each logits row). */
 int sg_row_stats(const float* logits_dev, int64_t row_stride, int32_t vocab,
                  int32_t num_rows, float* row_max_dev, float* row_sum_dev,

@@ -75,7 +75,11 @@ EXPORTED_SYMBOLS = (
     "sg_abi_version", "sg_last_error", "sg_abi_struct_size",
     "sg_tree_attn_plan", "sg_tree_attn_fwd", "sg_kv_commit",
     "sg_tree_sample", "sg_tree_sample_workspace_bytes", "sg_row_stats", "sg_exp_probe",
+    "sg_tree_sample_noalloc",
 )
+
+# Static scratch of sg_tree_sample_noalloc (SG_TREE_SAMPLE_NOALLOC_SCRATCH_BYTES).
+NOALLOC_SCRATCH_BYTES = 4 << 20
 
 _lib = None
 
@@ -111,6 +115,8 @@ def load() -> ctypes.CDLL:
     lib.sg_kv_commit.argtypes = [ctypes.POINTER(SgKvCommitArgs), c_void_p]
     lib.sg_tree_sample.restype = c_i32
     lib.sg_tree_sample.argtypes = [ctypes.POINTER(SgTreeSampleArgs), c_void_p]
+    lib.sg_tree_sample_noalloc.restype = c_i32
+    lib.sg_tree_sample_noalloc.argtypes = [ctypes.POINTER(SgTreeSampleArgs), c_void_p]
     lib.sg_tree_sample_workspace_bytes.restype = c_i64
     lib.sg_tree_sample_workspace_bytes.argtypes = [c_i32, c_i32]
     lib.sg_row_stats.restype = c_i32

@@ -697,9 +697,11 @@ extern "C" int64_t sg_tree_sample_workspace_bytes(int32_t num_requests, int32_t 
          static_cast<int64_t>(sizeof(float));
 }
 
-extern "C" int sg_tree_sample(const SgTreeSampleArgs* args, sg_stream_t stream) {
-  using namespace sg;
-  clear_error();
+namespace sg {
+namespace {
+
+// Checks every argument of sg_tree_sample except the workspace.
+int check_sample_args(const SgTreeSampleArgs* args) {
   SG_REQUIRE(args != nullptr, "null SgTreeSampleArgs");
   const SgTreeSampleArgs& a = *args;
   SG_REQUIRE(a.num_requests >= 0 && a.num_rows >= 0, "negative sizes");
@@ -713,10 +715,12 @@ extern "C" int sg_tree_sample(const SgTreeSampleArgs* args, sg_stream_t stream) 
                  a.uniforms_dev && a.row_max_dev && a.row_sum_dev && a.accept_len_dev &&
                  a.bonus_dev && (a.max_depth == 0 || a.accept_nodes_dev),
              "null device pointer");
-  SG_REQUIRE(a.workspace_dev != nullptr &&
-                 a.workspace_bytes >= sg_tree_sample_workspace_bytes(a.num_requests, a.vocab),
-             "workspace below sg_tree_sample_workspace_bytes");
-  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  return SG_OK;
+}
+
+// Enqueues the three kernels of one sampling call; a.workspace_dev holds at
+// least sg_tree_sample_workspace_bytes(num_requests, vocab) bytes.
+int launch_tree_sample(const SgTreeSampleArgs& a, hipStream_t s) {
   int rc = launch_row_stats(a.logits_dev, a.logits_row_stride, a.vocab, a.num_rows,
                             a.row_max_dev, a.row_sum_dev, s);
   if (rc != SG_OK) return rc;
@@ -737,6 +741,21 @@ extern "C" int sg_tree_sample(const SgTreeSampleArgs* args, sg_stream_t stream) 
   return SG_OK;
 }
 
+}  // namespace
+}  // namespace sg
+
+extern "C" int sg_tree_sample(const SgTreeSampleArgs* args, sg_stream_t stream) {
+  using namespace sg;
+  clear_error();
+  int rc = check_sample_args(args);
+  if (rc != SG_OK || args->num_requests == 0) return rc;
+  const SgTreeSampleArgs& a = *args;
+  SG_REQUIRE(a.workspace_dev != nullptr &&
+                 a.workspace_bytes >= sg_tree_sample_workspace_bytes(a.num_requests, a.vocab),
+             "workspace below sg_tree_sample_workspace_bytes");
+  return launch_tree_sample(a, reinterpret_cast<hipStream_t>(stream));
+}
+
 extern "C" int sg_exp_probe(const float* x_dev, float* out_dev, int64_t count,
                             sg_stream_t stream) {
   using namespace sg;
@@ -750,4 +769,67 @@ extern "C" int sg_exp_probe(const float* x_dev, float* out_dev, int64_t count,
                      reinterpret_cast<hipStream_t>(stream), x_dev, out_dev, count);
   SG_LAUNCH_CHECK();
   return SG_OK;
+}
+
+// ---------------------------------------------------------------------------
+// sg_tree_sample_noalloc: sg_tree_sample with its workspace in a static device
+// array, for callers that cannot allocate device memory.  Each GPU holds its
+// own copy of `scratch` (kNoAllocScratchBytes) until the process ends; its
+// device address is looked up once per device with hipGetSymbolAddress and
+// only that address is handed to the kernels (the array's name is a host-side
+// stand-in).  Every value the kernels read from it is written earlier in the
+// same call, so it needs no clearing; calls that overlap on one GPU race on it.
+// ---------------------------------------------------------------------------
+#include <mutex>
+
+static __device__ __align__(256) unsigned char scratch[SG_TREE_SAMPLE_NOALLOC_SCRATCH_BYTES];
+
+namespace sg {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_dev[kMaxDevices] = {};
+
+// Device address of the current device's copy of `scratch`.
+int current_scratch(void** out) {
+  int dev = -1;
+  SG_HIP_CHECK(hipGetDevice(&dev));
+  SG_REQUIRE(dev >= 0 && dev < kMaxDevices, "device index outside the scratch table");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* ptr = nullptr;
+    SG_HIP_CHECK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    SG_REQUIRE(ptr != nullptr, "hipGetSymbolAddress returned no address for the scratch");
+    g_scratch_dev[dev] = ptr;
+  }
+  *out = g_scratch_dev[dev];
+  return SG_OK;
+}
+
+}  // namespace
+}  // namespace sg
+
+extern "C" int sg_tree_sample_noalloc(const SgTreeSampleArgs* args, sg_stream_t stream) {
+  using namespace sg;
+  clear_error();
+  int rc = check_sample_args(args);
+  if (rc != SG_OK || args->num_requests == 0) return rc;
+  SG_REQUIRE(args->workspace_dev == nullptr && args->workspace_bytes == 0,
+             "sg_tree_sample_noalloc uses its own scratch: workspace_dev must be NULL "
+             "and workspace_bytes 0");
+  const int64_t need = sg_tree_sample_workspace_bytes(args->num_requests, args->vocab);
+  if (need > static_cast<int64_t>(SG_TREE_SAMPLE_NOALLOC_SCRATCH_BYTES))
+    return set_error(SG_EINVAL,
+                     "sg_tree_sample_noalloc: " + std::to_string(args->num_requests) +
+                         " requests over vocab " + std::to_string(args->vocab) + " need " +
+                         std::to_string(need) + " scratch bytes, above the static maximum of " +
+                         std::to_string(SG_TREE_SAMPLE_NOALLOC_SCRATCH_BYTES));
+  void* ws = nullptr;
+  rc = current_scratch(&ws);
+  if (rc != SG_OK) return rc;
+  SgTreeSampleArgs a = *args;
+  a.workspace_dev = ws;
+  a.workspace_bytes = SG_TREE_SAMPLE_NOALLOC_SCRATCH_BYTES;
+  return launch_tree_sample(a, reinterpret_cast<hipStream_t>(stream));
 }

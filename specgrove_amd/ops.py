@@ -268,15 +268,7 @@ class SampleResult:
     workspace: torch.Tensor | None = None  # per-slab complement totals of the exit rows
 
 
-def tree_sample(logits: torch.Tensor, row_offset: torch.Tensor, parent: torch.Tensor,
-                token: torch.Tensor, uniforms: torch.Tensor, max_depth: int,
-                out: SampleResult | None = None) -> SampleResult:
-    """Temperature-1 tree rejection sampling over all packed rows.
-
-    logits [R, V] fp32 (row-contiguous), row_offset [n+1] i32, parent/token
-    [R] i32 (request-local parents, -1 for roots), uniforms [n, U] fp32 with
-    U >= 2*(max_depth+1).
-    """
+def _check_sample_inputs(logits, row_offset, parent, token, uniforms, max_depth):
     _check_device_tensor(logits, "logits", torch.float32)
     _require(logits.dim() == 2 and logits.stride(1) == 1, "logits must be [R, V] row-contiguous")
     for t, name in ((row_offset, "row_offset"), (parent, "parent"), (token, "token")):
@@ -289,21 +281,11 @@ def tree_sample(logits: torch.Tensor, row_offset: torch.Tensor, parent: torch.Te
     _require(uniforms.shape[0] == n, "one uniform row per request")
     _require(uniforms.shape[1] >= 2 * (max_depth + 1), "uniforms must cover 2*(max_depth+1)")
     _require(parent.numel() >= rows and token.numel() >= rows, "parent/token must cover R rows")
-    dev = logits.device
-    if out is None:
-        depth_slots = max(max_depth, 1)
-        out = SampleResult(
-            accept_nodes=torch.empty((n, depth_slots), dtype=torch.int32, device=dev),
-            accept_len=torch.empty(n, dtype=torch.int32, device=dev),
-            bonus=torch.empty(n, dtype=torch.int32, device=dev),
-            keep_rows=torch.empty((n, max_depth + 1), dtype=torch.int32, device=dev),
-            row_max=torch.empty(rows, dtype=torch.float32, device=dev),
-            row_sum=torch.empty(rows, dtype=torch.float32, device=dev),
-            status=torch.zeros(1, dtype=torch.int32, device=dev),
-        )
-    ws_bytes = int(_lib.load().sg_tree_sample_workspace_bytes(n, logits.shape[1]))
-    if out.workspace is None or out.workspace.numel() < ws_bytes:
-        out.workspace = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+    return n, rows
+
+
+def _sample_args(logits, row_offset, parent, token, uniforms, max_depth, out, n, rows,
+                 workspace) -> "_lib.SgTreeSampleArgs":
     a = _lib.SgTreeSampleArgs()
     a.num_requests = n
     a.num_rows = rows
@@ -323,9 +305,53 @@ def tree_sample(logits: torch.Tensor, row_offset: torch.Tensor, parent: torch.Te
     a.bonus_dev = out.bonus.data_ptr()
     a.keep_rows_dev = out.keep_rows.data_ptr()
     a.status_dev = out.status.data_ptr()
-    a.workspace_dev = out.workspace.data_ptr()
-    a.workspace_bytes = out.workspace.numel()
+    a.workspace_dev = workspace.data_ptr() if workspace is not None else 0
+    a.workspace_bytes = workspace.numel() if workspace is not None else 0
+    return a
+
+
+def tree_sample(logits: torch.Tensor, row_offset: torch.Tensor, parent: torch.Tensor,
+                token: torch.Tensor, uniforms: torch.Tensor, max_depth: int,
+                out: SampleResult | None = None) -> SampleResult:
+    """Temperature-1 tree rejection sampling over all packed rows.
+
+    logits [R, V] fp32 (row-contiguous), row_offset [n+1] i32, parent/token
+    [R] i32 (request-local parents, -1 for roots), uniforms [n, U] fp32 with
+    U >= 2*(max_depth+1).
+    """
+    n, rows = _check_sample_inputs(logits, row_offset, parent, token, uniforms, max_depth)
+    dev = logits.device
+    if out is None:
+        depth_slots = max(max_depth, 1)
+        out = SampleResult(
+            accept_nodes=torch.empty((n, depth_slots), dtype=torch.int32, device=dev),
+            accept_len=torch.empty(n, dtype=torch.int32, device=dev),
+            bonus=torch.empty(n, dtype=torch.int32, device=dev),
+            keep_rows=torch.empty((n, max_depth + 1), dtype=torch.int32, device=dev),
+            row_max=torch.empty(rows, dtype=torch.float32, device=dev),
+            row_sum=torch.empty(rows, dtype=torch.float32, device=dev),
+            status=torch.zeros(1, dtype=torch.int32, device=dev),
+        )
+    ws_bytes = int(_lib.load().sg_tree_sample_workspace_bytes(n, logits.shape[1]))
+    if out.workspace is None or out.workspace.numel() < ws_bytes:
+        out.workspace = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+    a = _sample_args(logits, row_offset, parent, token, uniforms, max_depth, out, n, rows,
+                     out.workspace)
     _lib.check(_lib.load().sg_tree_sample(ctypes.byref(a), _stream_handle()), "sg_tree_sample")
+    return out
+
+
+def tree_sample_noalloc(logits: torch.Tensor, row_offset: torch.Tensor, parent: torch.Tensor,
+                        token: torch.Tensor, uniforms: torch.Tensor, max_depth: int,
+                        out: SampleResult) -> SampleResult:
+    """tree_sample through sg_tree_sample_noalloc: no device memory is
+    allocated (the library's static per-GPU scratch replaces the workspace);
+    the caller supplies every output in ``out`` (its ``workspace`` is unused)."""
+    n, rows = _check_sample_inputs(logits, row_offset, parent, token, uniforms, max_depth)
+    _require(isinstance(out, SampleResult), "sg_tree_sample_noalloc needs caller-owned outputs")
+    a = _sample_args(logits, row_offset, parent, token, uniforms, max_depth, out, n, rows, None)
+    _lib.check(_lib.load().sg_tree_sample_noalloc(ctypes.byref(a), _stream_handle()),
+               "sg_tree_sample_noalloc")
     return out
 
 
