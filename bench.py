@@ -9,22 +9,31 @@ input sets (each with its own >1 GB KV cache) rotate so the 256 MB
 Infinity Cache cannot serve repeated reads.
 
 Also reported in the same JSON line:
-  attention   per-call time of sg_tree_attn_fwd (HIP events on the launch stream),
-              rows/s, algorithmic GB/s and the fraction of 8 TB/s (= "roofline");
-  commit      per-call time of sg_kv_commit;
+  roofline    the attention kernel: algorithmic bytes / the average of calls
+              enqueued back to back between one pair of HIP events on the
+              launch stream (as the step loop runs them);
+  attention   that back-to-back time, the per-call (event-bracketed) median,
+              rows/s, GB/s, TFLOP/s of visible-key flops;
+  commit      one-layer and whole 36-layer-stack commit calls;
+  host        host (Python + ctypes) time to enqueue one step;
+  qwen3_4b    the Qwen3-4B-shape wave (16 requests, 512 rows), 16 rotating
+              input sets (1.2 GB);
+  tier128     a Qwen3-8B-shape wave of 128-node trees only (the MFMA-heaviest
+              units), 4 rotating input sets;
   sampler     tree sampling over 64 x 32 nodes, vocab 151936 (nodes/s, GB/s);
   long_context the heterogeneous long-context wave (128 requests, prefixes
               log-uniform 8k-32k, 4096 rows): attention, commit, and tree
               sampling over fp32 logits of every packed row (one input set);
   cpu_baseline the reference's CPU path restated (dense packed mask + SDPA in
-              fp32) on a bounded sample, timed on this host's cores.
+              fp32 with repeat_kv over all 64 requests), timed on this host's
+              cores; cpu_baseline_sampler likewise for fp32 softmax +
+              multinomial + walk over all 64 x 32 nodes.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
-import platform
 import statistics
 import sys
 import time
@@ -47,8 +56,6 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-sampler", action="store_true")
     p.add_argument("--no-long-context", action="store_true")
-    p.add_argument("--cpu-requests", type=int, default=16,
-                   help="requests in the CPU baseline's dense packed sample")
     p.add_argument("--target-units", type=int, default=0)
     p.add_argument("--counters-only", action="store_true",
                    help="for hardware-counter runs: --steps attention calls on the rotating "
@@ -72,8 +79,20 @@ def time_calls(torch, fn, iters):
     return [s.elapsed_time(e) for s, e in zip(starts, ends)]
 
 
-def build_attention_sets(torch, np, W, ops, device, steps_total):
-    wl = W.qwen3_8b_workload()
+def back_to_back(torch, fn, iters):
+    """Average milliseconds per call of ``iters`` calls enqueued back to back
+    between one pair of HIP events on the current (launch) stream."""
+    start, end = _events(torch, 2)
+    start.record()
+    for k in range(iters):
+        fn(k)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / iters
+
+
+def build_attention_sets(torch, np, W, ops, device, steps_total, wl=None, sets=N_SETS):
+    wl = W.qwen3_8b_workload() if wl is None else wl
     # headroom so every timed commit appends inside the slot
     max_keep = max(len(k) for k in wl.keep)
     wl.capacity = (int(wl.prefix_len.max()) + 128 + max_keep * (steps_total + 2) + 63) // 64 * 64
@@ -92,15 +111,45 @@ def build_attention_sets(torch, np, W, ops, device, steps_total):
     meta["keep_rows"] = torch.from_numpy(keep).to(device)
     meta["keep_len"] = torch.from_numpy(
         np.asarray([len(k) for k in wl.keep], np.int32)).to(device)
-    sets = []
-    for s in range(N_SETS):
+    input_sets = []
+    for s in range(sets):
         q, kc, vc, kt, vt = wl.make_tensors(device, seed=100 + s)
         out = torch.empty_like(q)
         lengths = meta["prefix_len"].clone()
         ptrs = [ops.pointer_array([t], device) for t in (kc, vc, kt, vt)]
-        sets.append(dict(q=q, kc=kc, vc=vc, kt=kt, vt=vt, out=out, lengths=lengths,
-                         ptrs=ptrs))
-    return wl, plan, meta, sets
+        input_sets.append(dict(q=q, kc=kc, vc=vc, kt=kt, vt=vt, out=out, lengths=lengths,
+                               ptrs=ptrs))
+    return wl, plan, meta, input_sets
+
+
+def attention_line(torch, np, W, ops, device, wl, sets, iters, warmup):
+    """Attention alone on a wave other than the step's: back-to-back and
+    per-call times over ``sets`` rotating input sets."""
+    wl, plan, meta, input_sets = build_attention_sets(torch, np, W, ops, device, 4, wl=wl,
+                                                      sets=sets)
+    call = lambda k: attention_call(ops, wl, plan, meta, input_sets[k % sets])  # noqa: E731
+    for k in range(warmup):
+        call(k)
+    torch.cuda.synchronize()
+    b2b = back_to_back(torch, call, iters)
+    per_call = time_calls(torch, call, iters)
+    nbytes, flops = wl.algorithmic_bytes(), wl.algorithmic_flops()
+    arena = sum(st["kc"].numel() * 2 * 2 for st in input_sets)
+    del input_sets
+    torch.cuda.empty_cache()
+    return {
+        "workload": f"{wl.name}: {wl.num_requests} requests, {wl.total_rows} rows, "
+                    f"{int(wl.prefix_len.sum())} prefix tokens, "
+                    f"{wl.num_q_heads}q/{wl.num_kv_heads}kv, D{wl.head_dim}",
+        "input_sets": sets, "input_bytes": arena,
+        "us_back_to_back": b2b * 1e3, "us_median_per_call": statistics.median(per_call) * 1e3,
+        "rows_per_s": wl.total_rows / (b2b * 1e-3),
+        "gbs": nbytes / (b2b * 1e-3) / 1e9, "frac": nbytes / (b2b * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "tflops": flops / (b2b * 1e-3) / 1e12,
+        "mfma_frac": flops / (b2b * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+        "algorithmic_bytes": nbytes, "algorithmic_flops": flops,
+        "plan_units": plan.units, "plan_merges": plan.merges,
+    }
 
 
 def attention_call(ops, wl, plan, meta, st):
@@ -178,9 +227,10 @@ def sampler_bench(torch, W, ops, device, iters, warmup):
     for k in range(warmup):
         call(k)
     torch.cuda.synchronize()
+    b2b = back_to_back(torch, call, iters)
     ms = time_calls(torch, call, iters)
     wl = sets[0]["wl"]
-    return wl, ms, sets
+    return wl, ms, sets, b2b
 
 
 def long_context_bench(torch, np, W, ops, device, iters=20, warmup=3):
@@ -224,6 +274,7 @@ def long_context_bench(torch, np, W, ops, device, iters=20, warmup=3):
     for k in range(warmup):
         attn(k)
     torch.cuda.synchronize()
+    attn_b2b = back_to_back(torch, attn, iters)
     attn_ms = time_calls(torch, attn, iters)
     commit_ms = time_calls(torch, commit, iters)
     del q, kc, vc, kt, vt, out, ptrs
@@ -247,84 +298,104 @@ def long_context_bench(torch, np, W, ops, device, iters=20, warmup=3):
     for k in range(2):
         sample(k)
     torch.cuda.synchronize()
-    samp_ms = time_calls(torch, sample, max(5, iters // 2))
+    samp_avg = back_to_back(torch, sample, max(5, iters // 2))
     del logits
     torch.cuda.empty_cache()
-    attn_avg, commit_avg, samp_avg = (statistics.fmean(x) for x in (attn_ms, commit_ms, samp_ms))
+    attn_avg = attn_b2b
+    commit_avg = statistics.fmean(commit_ms)
     abytes, sbytes = wl.algorithmic_bytes(), rows * vocab * 4
     return {
         "workload": "128 requests, prefixes log-uniform 8k-32k "
                     f"({int(wl.prefix_len.sum())} tokens), {rows} rows, 32q/8kv, D128",
-        "attention": {"us_avg": attn_avg * 1e3, "us_median": statistics.median(attn_ms) * 1e3,
+        "attention": {"us_back_to_back": attn_avg * 1e3,
+                      "us_median_per_call": statistics.median(attn_ms) * 1e3,
                       "rows_per_s": rows / (attn_avg * 1e-3),
                       "gbs": abytes / (attn_avg * 1e-3) / 1e9,
                       "frac": abytes / (attn_avg * 1e-3) / 1e9 / HBM_PEAK_GBS,
                       "algorithmic_bytes": abytes, "plan_units": plan.units,
                       "plan_merges": plan.merges},
         "commit": {"us_avg": commit_avg * 1e3, "rows": int(sum(len(k) for k in wl.keep))},
-        "sampler": {"us_avg": samp_avg * 1e3, "nodes_per_s": rows / (samp_avg * 1e-3),
+        "sampler": {"us_back_to_back": samp_avg * 1e3, "nodes_per_s": rows / (samp_avg * 1e-3),
                     "gbs": sbytes / (samp_avg * 1e-3) / 1e9,
                     "frac": sbytes / (samp_avg * 1e-3) / 1e9 / HBM_PEAK_GBS,
                     "algorithmic_bytes": sbytes},
     }
 
 
-def cpu_attention_baseline(torch, np, W, requests):
-    """Reference wave restated on the CPU: dense packed mask + fp32 SDPA."""
+def cpu_attention_baseline(torch, np, W, row_block=128, budget_s=60.0):
+    """Reference wave restated on the CPU over the whole Qwen3-8B wave: the
+    dense packed mask [R, P+R] + fp32 SDPA with repeat_kv
+    (continuous_tree_block_decode.py:500-546 -> transformers' SDPA), run in
+    blocks of ``row_block`` query rows (each row still scores all P+R keys).
+    Blocks cost the same, so if the projected time exceeds ``budget_s`` the
+    run stops early and the rate is that of the blocks done."""
     from oracle import oracle
     threads = oracle.cpu_threads()
     torch.set_num_threads(threads)
     wl = W.qwen3_8b_workload()
-    sub = list(range(requests))
     q, kc, vc, kt, vt = wl.make_tensors("cpu", seed=100)
-    rows = wl.row_offset
-    q_sub = torch.cat([q[rows[i]:rows[i + 1]] for i in sub])
-    kt_sub = torch.cat([kt[rows[i]:rows[i + 1]] for i in sub])
-    vt_sub = torch.cat([vt[rows[i]:rows[i + 1]] for i in sub])
-    ks = [kc[:, int(wl.prefix_start[i]):int(wl.prefix_start[i]) + int(wl.prefix_len[i])]
-          for i in sub]
-    vs = [vc[:, int(wl.prefix_start[i]):int(wl.prefix_start[i]) + int(wl.prefix_len[i])]
-          for i in sub]
-    parents = [wl.parents[i] for i in sub]
+    ks = [kc[:, int(s):int(s) + int(L)] for s, L in zip(wl.prefix_start, wl.prefix_len)]
+    vs = [vc[:, int(s):int(s) + int(L)] for s, L in zip(wl.prefix_start, wl.prefix_len)]
+    rows = wl.total_rows
     t0 = time.perf_counter()
-    oracle.attention_dense(q_sub, ks, vs, kt_sub, vt_sub, parents)
+    wave = oracle.DenseWave(q, ks, vs, kt, vt, wl.parents)
+    setup = time.perf_counter() - t0
+    done = 0
+    while done < rows:
+        wave(done, min(rows, done + row_block))
+        done = min(rows, done + row_block)
+        elapsed = time.perf_counter() - t0
+        if setup + (elapsed - setup) / done * rows > budget_s and done < rows:
+            break
+    # Rows/s of the whole wave: the one-time packing plus the blocks done,
+    # scaled to all rows.
     elapsed = time.perf_counter() - t0
-    n_rows = int(q_sub.shape[0])
-    return dict(value=n_rows / elapsed, unit="rows/s", cores=threads, kind="port",
-                sample=(f"dense packed wave of the first {requests} of 64 requests "
-                        f"({n_rows} rows, {int(sum(wl.prefix_len[:requests]))} prefix keys), "
-                        f"fp32 torch SDPA with additive mask and repeat_kv, "
-                        f"{elapsed:.2f} s on {platform.processor() or platform.machine()}"))
+    per_row = (elapsed - setup) / done
+    wave_s = setup + per_row * rows
+    keys = int(wl.prefix_len.sum()) + rows
+    return dict(value=rows / wave_s, unit="rows/s", cores=threads, kind="port",
+                sample=(f"dense packed wave of all 64 requests ({rows} rows x {keys} keys, "
+                        f"mask [R, P+R]), fp32 torch SDPA with repeat_kv in {row_block}-row "
+                        f"blocks: packing {setup:.1f} s + {done} of {rows} rows in "
+                        f"{elapsed - setup:.1f} s (wave {wave_s:.1f} s)"),
+                cpu_model=oracle.cpu_model())
 
 
-def cpu_sampler_baseline(torch, np, sets, requests=16):
-    """Reference sampling stage on the CPU: fp32 softmax of the rows, one
-    multinomial per request, ancestral walk."""
+def cpu_sampler_baseline(torch, np, sets):
+    """Reference sampling stage on the CPU over all 64 x 32 nodes: fp32
+    softmax of the rows (sampling.py:29-36), one multinomial per request and
+    the ancestral walk (sampling.py:903-950)."""
     from oracle import oracle
     threads = oracle.cpu_threads()
     torch.set_num_threads(threads)
     st = sets[0]
     wl = st["wl"]
+    requests = len(wl.parents)
     rows = int(wl.row_offset[requests])
     logits = st["logits"][:rows].cpu()
     t0 = time.perf_counter()
-    oracle.reference_sampling_wave(logits, wl.row_offset[:requests + 1],
-                                   wl.parents[:requests], wl.tokens[:requests],
+    oracle.reference_sampling_wave(logits, wl.row_offset, wl.parents, wl.tokens,
                                    list(range(requests)))
     elapsed = time.perf_counter() - t0
     return dict(value=rows / elapsed, unit="nodes/s", cores=threads, kind="port",
-                sample=f"{requests} of 64 requests ({rows} nodes, vocab {wl.vocab}): fp32 "
-                       f"softmax + multinomial + walk, {elapsed:.2f} s")
+                sample=f"all {requests} requests ({rows} nodes, vocab {wl.vocab}): fp32 "
+                       f"softmax + multinomial + walk, {elapsed:.2f} s",
+                cpu_model=oracle.cpu_model())
 
 
 def read_traffic():
+    """HBM bytes per attention launch from the committed counter profile, with
+    the commit and box it was measured on (counters need a rocprofv3 run of
+    their own; see the profile for the commands)."""
     path = ROOT / "profiles" / "tree_attn_qwen3_8b_traffic.json"
     if not path.exists():
-        return None
+        return None, None
     try:
-        return json.loads(path.read_text()).get("hbm_bytes_per_launch")
+        data = json.loads(path.read_text())
     except (ValueError, OSError):
-        return None
+        return None, None
+    source = {k: data.get(k) for k in ("measured_at_commit", "box", "commands")}
+    return data.get("hbm_bytes_per_launch"), source
 
 
 def counters_only(torch, np, W, ops, device, steps, warmup):
@@ -360,7 +431,7 @@ def main():
         counters_only(torch, np, W, ops, device, steps, warmup)
         return
     wl, plan, meta, sets = build_attention_sets(torch, np, W, ops, device,
-                                                3 * (steps + warmup) + 16)
+                                                4 * (steps + warmup) + 16)
     rows = wl.total_rows
 
     def step(k):
@@ -379,15 +450,24 @@ def main():
     torch.cuda.synchronize()
     ms_per_step = start.elapsed_time(end) / steps
 
-    attn_ms = time_calls(torch, lambda k: attention_call(ops, wl, plan, meta, sets[k % N_SETS]),
-                         steps)
-    commit_ms = time_calls(torch, lambda k: commit_call(ops, wl, meta, sets[k % N_SETS]), steps)
-    attn_avg = statistics.fmean(attn_ms)
-    attn_med = statistics.median(attn_ms)
+    # Host time to enqueue one step (argument checks, ctypes, launches); the
+    # GPU runs behind, so this is the host's share, not the step's duration.
+    t0 = time.perf_counter()
+    for k in range(steps):
+        step(k)
+    host_us = (time.perf_counter() - t0) / steps * 1e6
+    torch.cuda.synchronize()
+
+    attn_call = lambda k: attention_call(ops, wl, plan, meta, sets[k % N_SETS])  # noqa: E731
+    attn_b2b = back_to_back(torch, attn_call, steps)
+    attn_ms = time_calls(torch, attn_call, steps)
+    commit_one = lambda k: commit_call(ops, wl, meta, sets[k % N_SETS])  # noqa: E731
+    commit_b2b = back_to_back(torch, commit_one, steps)
+    commit_ms = time_calls(torch, commit_one, steps)
     attn_bytes = wl.algorithmic_bytes()
     attn_flops = wl.algorithmic_flops()
-    achieved = attn_bytes / (attn_avg * 1e-3) / 1e9
-    commit_avg = statistics.fmean(commit_ms)
+    achieved = attn_bytes / (attn_b2b * 1e-3) / 1e9
+    traffic, traffic_source = read_traffic()
 
     result = {
         "metric": "packed-verify rows/s at Qwen3-8B shape; % HBM roofline; tree-sample nodes/s",
@@ -417,48 +497,57 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": read_traffic(),
+            "traffic": traffic,
+            "traffic_source": traffic_source,
             "kernel": "sg_tree_attn_fwd (tree_attn_kernel<128> + merge)",
             "algorithmic_bytes": attn_bytes,
+            "timing": f"{steps} calls back to back between one pair of HIP events",
         },
         "attention": {
-            "us_avg": attn_avg * 1e3,
-            "us_median": attn_med * 1e3,
-            "rows_per_s": rows / (attn_avg * 1e-3),
+            "us_back_to_back": attn_b2b * 1e3,
+            "us_median_per_call": statistics.median(attn_ms) * 1e3,
+            "rows_per_s": rows / (attn_b2b * 1e-3),
             "gbs": achieved,
-            "tflops": attn_flops / (attn_avg * 1e-3) / 1e12,
-            "mfma_frac": attn_flops / (attn_avg * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+            "tflops": attn_flops / (attn_b2b * 1e-3) / 1e12,
+            "mfma_frac": attn_flops / (attn_b2b * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+            "algorithmic_flops": attn_flops,
             "plan_units": plan.units,
             "plan_merges": plan.merges,
         },
         "commit": {
-            "us_avg": commit_avg * 1e3,
+            "us_back_to_back": commit_b2b * 1e3,
+            "us_median_per_call": statistics.median(commit_ms) * 1e3,
             "rows": int(sum(len(k) for k in wl.keep)),
-            "gbs": wl.commit_bytes() / (commit_avg * 1e-3) / 1e9,
+            "gbs": wl.commit_bytes() / (commit_b2b * 1e-3) / 1e9,
             "all_layers": commit_all_layers(torch, np, ops, wl, meta, device),
         },
+        "host": {"us_per_step_enqueue": host_us},
     }
+    del sets
+    torch.cuda.empty_cache()
+    result["qwen3_4b"] = attention_line(torch, np, W, ops, device, W.qwen3_4b_workload(), 16,
+                                        steps, warmup)
+    result["tier128"] = attention_line(torch, np, W, ops, device, W.tier128_workload(), 4,
+                                       steps, warmup)
 
     samp_sets = None
     if not args.no_sampler:
-        swl, samp_ms, samp_sets = sampler_bench(torch, W, ops, device, steps, warmup)
-        savg = statistics.fmean(samp_ms)
+        swl, samp_ms, samp_sets, samp_b2b = sampler_bench(torch, W, ops, device, steps, warmup)
         sbytes = swl.algorithmic_bytes()
         result["sampler"] = {
             "workload": swl.name,
-            "us_avg": savg * 1e3,
-            "us_median": statistics.median(samp_ms) * 1e3,
-            "nodes_per_s": swl.total_rows / (savg * 1e-3),
-            "gbs": sbytes / (savg * 1e-3) / 1e9,
-            "frac": sbytes / (savg * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "us_back_to_back": samp_b2b * 1e3,
+            "us_median_per_call": statistics.median(samp_ms) * 1e3,
+            "nodes_per_s": swl.total_rows / (samp_b2b * 1e-3),
+            "gbs": sbytes / (samp_b2b * 1e-3) / 1e9,
+            "frac": sbytes / (samp_b2b * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "algorithmic_bytes": sbytes,
         }
     if not args.no_long_context:
-        del sets
         torch.cuda.empty_cache()
         result["long_context"] = long_context_bench(torch, np, W, ops, device)
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_attention_baseline(torch, np, W, args.cpu_requests)
+        result["cpu_baseline"] = cpu_attention_baseline(torch, np, W)
         if samp_sets is not None:
             result["cpu_baseline_sampler"] = cpu_sampler_baseline(torch, np, samp_sets)
     print(json.dumps(result), flush=True)

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define SG_ABI_VERSION 2
+#define SG_ABI_VERSION 3
 
 #define SG_OK 0
 #define SG_EINVAL (-1)  /* shape or contract violation (Python: ValueError) */
@@ -35,6 +35,12 @@ extern "C" {
 #define SG_EHIP (-3)    /* HIP launch/runtime error (Python: RuntimeError) */
 
 typedef struct ihipStream_t* sg_stream_t; /* == hipStream_t */
+
+/* Element types of the sampler's logits.  bf16 and f16 widen to fp32 exactly,
+ * so their statistics and decisions equal those of the widened fp32 rows. */
+#define SG_DTYPE_F32 0
+#define SG_DTYPE_BF16 1
+#define SG_DTYPE_F16 2
 
 /* ABI version (SG_ABI_VERSION).  No reference counterpart. */
 int sg_abi_version(void);
@@ -56,9 +62,9 @@ const char* sg_last_error(void);
  * ---------------------------------------------------------------------- */
 typedef struct SgTreeAttnArgs {
   int32_t num_requests;   /* n */
-  int32_t num_rows;       /* R = row_offset[n] */
+  int32_t num_rows;       /* R = row_offset[n]: rows of q, k/v_tree and out */
   int32_t num_q_heads;    /* Hq */
-  int32_t num_kv_heads;   /* Hkv; Hq % Hkv == 0, Hq/Hkv <= 8 */
+  int32_t num_kv_heads;   /* Hkv; Hq % Hkv == 0 and 1 <= Hq/Hkv <= 16 */
   int32_t head_dim;       /* D: 64 or 128 */
   float scale;            /* softmax scale, usually D^-0.5 */
   /* queries [R, Hq, D] bf16 */
@@ -75,17 +81,24 @@ typedef struct SgTreeAttnArgs {
   /* request metadata (device, int32) */
   const int32_t* row_offset_dev;   /* [n+1] */
   const int64_t* prefix_start_dev; /* [n] first cache token of request i (slot*capacity) */
-  const int32_t* prefix_len_dev;   /* [n] cached prefix length L_i */
+  const int32_t* prefix_len_dev;   /* [n] cached prefix length L_i; every unit checks its
+                                      key range and rows against L_i and row_offset */
   const int32_t* parent_dev;       /* [R] request-local parent row, -1 for the root */
   /* output [R, Hq, D] bf16 */
   void* out_dev;
   int64_t out_row_stride, out_head_stride;
   /* work plan from sg_tree_attn_plan (device copy) and its scratch */
   const void* plan_dev;
+  const void* plan_host; /* optional host copy of the same plan: its header is checked
+                            against these arguments before anything is enqueued */
   int32_t plan_units;    /* work lists = workgroups of the first kernel */
   int32_t plan_merges;   /* split-K merge groups (second kernel's grid) */
   void* workspace_dev;
   size_t workspace_bytes;
+  int32_t* status_dev;   /* optional [1] device word, never cleared by the library: set
+                            to SG_EINVAL when a unit's key range or rows disagree with
+                            prefix_len_dev / row_offset_dev (a plan of another wave); that
+                            unit reads no K/V and writes NaN to its output rows */
 } SgTreeAttnArgs;
 
 /* Host-side planner.  From host copies of row_offset [n+1] and prefix_len [n]
@@ -104,6 +117,14 @@ int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset_host,
                       size_t plan_capacity_bytes, size_t* plan_bytes,
                       int32_t* plan_units, int32_t* plan_merges,
                       size_t* workspace_bytes);
+
+/* SG_OK when plan_host was built by sg_tree_attn_plan from exactly these
+ * row offsets and prefix lengths (the plan header keeps their count, the row
+ * total and a 64-bit hash of both arrays), SG_EINVAL otherwise.  A plan is
+ * per wave: prefix lengths change after every commit.  No reference
+ * counterpart (the reference rebuilds its dense mask every wave). */
+int sg_tree_attn_plan_check(const void* plan_host, int32_t num_requests,
+                            const int32_t* row_offset_host, const int32_t* prefix_len_host);
 
 /* Enqueue the attention of one layer. */
 int sg_tree_attn_fwd(const SgTreeAttnArgs* args, sg_stream_t stream);
@@ -164,9 +185,13 @@ typedef struct SgTreeSampleArgs {
   int32_t num_rows;
   int32_t vocab;              /* V <= 524288 */
   int32_t max_depth;          /* accept_nodes slots per request */
-  const float* logits_dev;    /* [R, logits_row_stride] fp32 target logits (T = 1) */
-  int64_t logits_row_stride;
-  const int32_t* row_offset_dev; /* [n+1] */
+  int32_t logits_dtype;       /* SG_DTYPE_F32, SG_DTYPE_BF16 or SG_DTYPE_F16 (the
+                                 reference's logits kernels take f16/bf16/f32,
+                                 FTS:941-1301) */
+  const void* logits_dev;     /* [R, logits_row_stride] target logits (T = 1) */
+  int64_t logits_row_stride;  /* elements */
+  const int32_t* row_offset_dev; /* [n+1]; row_offset[n] <= num_rows (a request
+                                    outside the num_rows rows is a broken walk) */
   const int32_t* parent_dev;     /* [R] local parent, -1 for roots */
   const int32_t* token_dev;      /* [R] draft token of each node (root entry unused) */
   const float* uniforms_dev;     /* [n, uniform_stride] fp32 in [0,1) */
@@ -177,7 +202,8 @@ typedef struct SgTreeSampleArgs {
   int32_t* accept_len_dev;       /* [n] */
   int32_t* bonus_dev;            /* [n] */
   int32_t* keep_rows_dev;        /* optional [n, max_depth+1]: [0] + nodes, -1 padded */
-  int32_t* status_dev;           /* optional [1]: SG_EINVAL if a walk broke the contract */
+  int32_t* status_dev;           /* optional [1]: cleared to 0 by the call, then
+                                    SG_EINVAL if a walk broke the contract */
   void* workspace_dev;           /* >= sg_tree_sample_workspace_bytes(): per-slab
                                     and per-line complement totals of the exit rows,
                                     and each request's exit node and its children */
@@ -208,8 +234,8 @@ int64_t sg_tree_sample_workspace_bytes(int32_t num_requests, int32_t vocab);
 int sg_tree_sample_noalloc(const SgTreeSampleArgs* args, sg_stream_t stream);
 
 /* Row statistics only (max and sum of exp of each logits row). */
-int sg_row_stats(const float* logits_dev, int64_t row_stride, int32_t vocab,
-                 int32_t num_rows, float* row_max_dev, float* row_sum_dev,
+int sg_row_stats(const void* logits_dev, int32_t logits_dtype, int64_t row_stride,
+                 int32_t vocab, int32_t num_rows, float* row_max_dev, float* row_sum_dev,
                  sg_stream_t stream);
 
 /* sizeof() of the argument structs as compiled into the library, for binding

@@ -111,13 +111,15 @@ def complement_draw(row: np.ndarray, m: float, child_tokens: Sequence[int],
 
 
 def tree_sample(logits: np.ndarray, row_offset: np.ndarray, parent: np.ndarray,
-                token: np.ndarray, uniforms: np.ndarray, max_depth: int):
+                token: np.ndarray, uniforms: np.ndarray, max_depth: int,
+                threads: int = 1):
     """Oracle for the packed sampler.
 
     ``logits`` [rows, V] fp32, ``row_offset`` [n+1], ``parent``/``token``
     [rows] int32 (request-local parent, -1 root), ``uniforms`` [n, U] fp32.
     Returns (accept_nodes [n, max_depth], accept_len [n], bonus [n],
-    row_m [rows], row_z [rows]).
+    row_m [rows], row_z [rows]).  Requests are independent, so ``threads`` > 1
+    runs contiguous groups of requests in parallel C calls (same results).
     """
     logits = np.ascontiguousarray(logits, dtype=np.float32)
     row_offset = np.ascontiguousarray(row_offset, dtype=np.int32)
@@ -126,7 +128,7 @@ def tree_sample(logits: np.ndarray, row_offset: np.ndarray, parent: np.ndarray,
     uniforms = np.ascontiguousarray(uniforms, dtype=np.float32)
     n = row_offset.size - 1
     rows = int(row_offset[-1])
-    if logits.ndim != 2 or logits.shape[0] < rows:
+    if logits.ndim != 2 or logits.shape[0] < rows or int(row_offset[0]) != 0:
         raise ValueError("logits do not cover the packed rows")
     depth_slots = max(int(max_depth), 1)
     nodes = np.full((n, depth_slots), -1, np.int32)
@@ -134,13 +136,26 @@ def tree_sample(logits: np.ndarray, row_offset: np.ndarray, parent: np.ndarray,
     bonus = np.zeros(n, np.int32)
     row_m = np.zeros(rows, np.float32)
     row_z = np.zeros(rows, np.float32)
-    status = lib().sgo_tree_sample(
-        _f32p(logits), logits.shape[1], logits.shape[1], n, _i32p(row_offset),
-        _i32p(parent), _i32p(token), _f32p(uniforms), uniforms.shape[1],
-        int(max_depth), _i32p(nodes), _i32p(length), _i32p(bonus),
-        _f32p(row_m), _f32p(row_z),
-    )
-    if status != 0:
+    vocab = logits.shape[1]
+
+    def run(a: int, b: int) -> int:
+        r0, r1 = int(row_offset[a]), int(row_offset[b])
+        ro = np.ascontiguousarray(row_offset[a:b + 1] - r0)
+        return lib().sgo_tree_sample(
+            _f32p(logits[r0:r1]), vocab, vocab, b - a, _i32p(ro),
+            _i32p(parent[r0:r1]), _i32p(token[r0:r1]), _f32p(uniforms[a:b]),
+            uniforms.shape[1], int(max_depth), _i32p(nodes[a:b]), _i32p(length[a:b]),
+            _i32p(bonus[a:b]), _f32p(row_m[r0:r1]), _f32p(row_z[r0:r1]),
+        )
+
+    if threads > 1 and n > 1:
+        from concurrent.futures import ThreadPoolExecutor
+        bounds = np.linspace(0, n, min(threads, n) + 1).astype(int)
+        with ThreadPoolExecutor(len(bounds) - 1) as pool:  # ctypes releases the GIL
+            statuses = list(pool.map(run, bounds[:-1], bounds[1:]))
+    else:
+        statuses = [run(0, n)] if n > 0 else [0]
+    if any(status != 0 for status in statuses):
         raise ValueError("oracle sampler rejected its inputs")
     return nodes[:, :max_depth], length, bonus, row_m, row_z
 
@@ -219,34 +234,59 @@ def packed_ids_positions(roots: Sequence[int], tokens_list, depths_list,
 # Attention (transformers sdpa_attention_forward with an explicit mask)
 # --------------------------------------------------------------------------
 
+class DenseWave:
+    """The reference packed wave's attention inputs, built once: all prefixes
+    and tree rows concatenated into one packed K/V (``_pack_cache_sequence``),
+    expanded to every query head (transformers' ``repeat_kv``), and the dense
+    additive mask [R, P+R] (``_packed_block_inputs``), all fp32 on the CPU
+    (CTBD:313-361, :500-546).  Calling it runs the masked SDPA for query rows
+    [a, b) over all P+R keys."""
+
+    def __init__(self, q, k_prefix_list, v_prefix_list, k_tree, v_tree, parents_list,
+                 scale: float | None = None):
+        import torch
+        self.q = torch.as_tensor(q).float()
+        rows, hq, dim = self.q.shape
+        hkv = k_tree.shape[1]
+        group = hq // hkv
+        lengths = [int(k.shape[1]) for k in k_prefix_list]
+        keys = torch.cat([torch.as_tensor(k).float() for k in k_prefix_list]
+                         + [torch.as_tensor(k_tree).float().transpose(0, 1)], dim=1)
+        values = torch.cat([torch.as_tensor(v).float() for v in v_prefix_list]
+                           + [torch.as_tensor(v_tree).float().transpose(0, 1)], dim=1)
+        self.mask = torch.from_numpy(packed_dense_mask(lengths, parents_list))
+        self.keys = keys.repeat_interleave(group, dim=0).unsqueeze(0)
+        self.values = values.repeat_interleave(group, dim=0).unsqueeze(0)
+        self.scale = dim ** -0.5 if scale is None else scale
+        self.rows = rows
+
+    def __call__(self, a: int, b: int):
+        """[b - a, Hq, D] fp32 output of query rows [a, b)."""
+        import torch
+        out = torch.nn.functional.scaled_dot_product_attention(
+            self.q[a:b].transpose(0, 1).unsqueeze(0), self.keys, self.values,
+            attn_mask=self.mask[a:b], scale=self.scale,
+        )
+        return out[0].transpose(0, 1)
+
+
 def attention_dense(q, k_prefix_list, v_prefix_list, k_tree, v_tree,
-                    parents_list, scale: float | None = None):
+                    parents_list, scale: float | None = None,
+                    row_block: int | None = None):
     """Reference packed wave: one dense masked SDPA over all P+R keys.
 
     q [R, Hq, D]; k/v_prefix_list[i] [Hkv, L_i, D]; k/v_tree [R, Hkv, D].
     All inputs are upcast to fp32 (they hold bf16 values).  Returns [R, Hq, D]
     fp32.  Mirrors _pack_cache_sequence + _packed_block_inputs + repeat_kv +
     F.scaled_dot_product_attention(attn_mask=mask) (CTBD:313-361, :500-546).
+    ``row_block`` runs the same SDPA on blocks of that many query rows (each
+    row still scores all P+R keys), which bounds the score matrix's memory.
     """
     import torch
-    q = torch.as_tensor(q).float()
-    rows, hq, dim = q.shape
-    hkv = k_tree.shape[1]
-    group = hq // hkv
-    lengths = [int(k.shape[1]) for k in k_prefix_list]
-    keys = torch.cat([torch.as_tensor(k).float() for k in k_prefix_list]
-                     + [torch.as_tensor(k_tree).float().transpose(0, 1)], dim=1)
-    values = torch.cat([torch.as_tensor(v).float() for v in v_prefix_list]
-                       + [torch.as_tensor(v_tree).float().transpose(0, 1)], dim=1)
-    mask = torch.from_numpy(packed_dense_mask(lengths, parents_list))
-    keys = keys.repeat_interleave(group, dim=0)
-    values = values.repeat_interleave(group, dim=0)
-    scale = dim ** -0.5 if scale is None else scale
-    out = torch.nn.functional.scaled_dot_product_attention(
-        q.transpose(0, 1).unsqueeze(0), keys.unsqueeze(0), values.unsqueeze(0),
-        attn_mask=mask, scale=scale,
-    )
-    return out[0].transpose(0, 1).contiguous()
+    wave = DenseWave(q, k_prefix_list, v_prefix_list, k_tree, v_tree, parents_list, scale)
+    block = wave.rows if not row_block else int(row_block)
+    pieces = [wave(a, min(wave.rows, a + block)) for a in range(0, wave.rows, block)]
+    return torch.cat(pieces, dim=0).contiguous() if len(pieces) > 1 else pieces[0].contiguous()
 
 
 def attention_per_request(q, k_prefix_list, v_prefix_list, k_tree, v_tree,
@@ -254,6 +294,11 @@ def attention_per_request(q, k_prefix_list, v_prefix_list, k_tree, v_tree,
                           requests: Sequence[int] | None = None):
     """Same math as attention_dense restricted to each request's own keys.
 
+    Per kv head g the request's G query heads are stacked into one [n*G, D]
+    operand (row r, head h at r*G + h), scored against the prefix keys and the
+    request's tree keys, masked to ancestors-or-self on the tree part,
+    soft-maxed in fp32 and applied to the values: the same visible sets and
+    GQA mapping as the dense wave, as plain fp32 matrix products.
     Returns a dict request -> [n_i, Hq, D] fp32 (only ``requests`` if given).
     """
     import torch
@@ -269,21 +314,19 @@ def attention_per_request(q, k_prefix_list, v_prefix_list, k_tree, v_tree,
         n = r1 - r0
         kp = torch.as_tensor(k_prefix_list[i]).float()
         vp = torch.as_tensor(v_prefix_list[i]).float()
-        kt = torch.as_tensor(k_tree[r0:r1]).float().transpose(0, 1)
-        vt = torch.as_tensor(v_tree[r0:r1]).float().transpose(0, 1)
-        keys = torch.cat([kp, kt], dim=1).repeat_interleave(group, dim=0)
-        values = torch.cat([vp, vt], dim=1).repeat_interleave(group, dim=0)
         length = kp.shape[1]
-        mask = torch.full((n, length + n), -math.inf)
-        mask[:, :length] = 0
-        vis = torch.from_numpy(visibility(parents_list[i]))
-        mask[:, length:][vis] = 0
-        qi = q[r0:r1].float().transpose(0, 1).unsqueeze(0)
-        o = torch.nn.functional.scaled_dot_product_attention(
-            qi, keys.unsqueeze(0), values.unsqueeze(0), attn_mask=mask,
-            scale=scale,
-        )
-        out[i] = o[0].transpose(0, 1).contiguous()
+        hidden = ~torch.from_numpy(visibility(parents_list[i])).repeat_interleave(group, 0)
+        qi = q[r0:r1].float()
+        o = torch.empty(n, hq, dim)
+        for g in range(hkv):
+            qg = qi[:, g * group:(g + 1) * group].reshape(n * group, dim)
+            kg = torch.cat([kp[g], torch.as_tensor(k_tree[r0:r1, g]).float()])
+            vg = torch.cat([vp[g], torch.as_tensor(v_tree[r0:r1, g]).float()])
+            scores = (qg @ kg.T) * scale
+            scores[:, length:].masked_fill_(hidden, -math.inf)
+            o[:, g * group:(g + 1) * group] = (
+                torch.softmax(scores, dim=-1) @ vg).reshape(n, group, dim)
+        out[i] = o
     return out
 
 
@@ -348,6 +391,19 @@ def kv_commit(arena_k: np.ndarray, arena_v: np.ndarray, lengths: np.ndarray,
             arena_v[:, :, base + t] = tree_v[:, src]
         lengths[slot] += len(keep)
     return lengths
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (from /proc/cpuinfo when available)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or platform.machine()
 
 
 def cpu_threads() -> int:

@@ -16,6 +16,11 @@ SG_EINVAL = -1
 SG_ERANGE = -2
 SG_EHIP = -3
 
+SG_ABI_VERSION = 3
+SG_DTYPE_F32 = 0
+SG_DTYPE_BF16 = 1
+SG_DTYPE_F16 = 2
+
 c_void_p = ctypes.c_void_p
 c_i32 = ctypes.c_int32
 c_i64 = ctypes.c_int64
@@ -35,8 +40,9 @@ class SgTreeAttnArgs(ctypes.Structure):
         ("row_offset_dev", c_void_p), ("prefix_start_dev", c_void_p),
         ("prefix_len_dev", c_void_p), ("parent_dev", c_void_p),
         ("out_dev", c_void_p), ("out_row_stride", c_i64), ("out_head_stride", c_i64),
-        ("plan_dev", c_void_p), ("plan_units", c_i32), ("plan_merges", c_i32),
-        ("workspace_dev", c_void_p), ("workspace_bytes", c_size),
+        ("plan_dev", c_void_p), ("plan_host", c_void_p), ("plan_units", c_i32),
+        ("plan_merges", c_i32), ("workspace_dev", c_void_p), ("workspace_bytes", c_size),
+        ("status_dev", c_void_p),
     ]
 
 
@@ -58,7 +64,7 @@ class SgKvCommitArgs(ctypes.Structure):
 class SgTreeSampleArgs(ctypes.Structure):
     _fields_ = [
         ("num_requests", c_i32), ("num_rows", c_i32), ("vocab", c_i32),
-        ("max_depth", c_i32),
+        ("max_depth", c_i32), ("logits_dtype", c_i32),
         ("logits_dev", c_void_p), ("logits_row_stride", c_i64),
         ("row_offset_dev", c_void_p), ("parent_dev", c_void_p),
         ("token_dev", c_void_p), ("uniforms_dev", c_void_p),
@@ -75,7 +81,7 @@ EXPORTED_SYMBOLS = (
     "sg_abi_version", "sg_last_error", "sg_abi_struct_size",
     "sg_tree_attn_plan", "sg_tree_attn_fwd", "sg_kv_commit",
     "sg_tree_sample", "sg_tree_sample_workspace_bytes", "sg_row_stats", "sg_exp_probe",
-    "sg_tree_sample_noalloc",
+    "sg_tree_sample_noalloc", "sg_tree_attn_plan_check",
 )
 
 # Static scratch of sg_tree_sample_noalloc (SG_TREE_SAMPLE_NOALLOC_SCRATCH_BYTES).
@@ -109,6 +115,9 @@ def load() -> ctypes.CDLL:
         c_void_p, c_size, ctypes.POINTER(c_size), ctypes.POINTER(c_i32),
         ctypes.POINTER(c_i32), ctypes.POINTER(c_size),
     ]
+    lib.sg_tree_attn_plan_check.restype = c_i32
+    lib.sg_tree_attn_plan_check.argtypes = [c_void_p, c_i32, ctypes.POINTER(c_i32),
+                                            ctypes.POINTER(c_i32)]
     lib.sg_tree_attn_fwd.restype = c_i32
     lib.sg_tree_attn_fwd.argtypes = [ctypes.POINTER(SgTreeAttnArgs), c_void_p]
     lib.sg_kv_commit.restype = c_i32
@@ -120,9 +129,15 @@ def load() -> ctypes.CDLL:
     lib.sg_tree_sample_workspace_bytes.restype = c_i64
     lib.sg_tree_sample_workspace_bytes.argtypes = [c_i32, c_i32]
     lib.sg_row_stats.restype = c_i32
-    lib.sg_row_stats.argtypes = [c_void_p, c_i64, c_i32, c_i32, c_void_p, c_void_p, c_void_p]
+    lib.sg_row_stats.argtypes = [c_void_p, c_i32, c_i64, c_i32, c_i32, c_void_p, c_void_p,
+                                 c_void_p]
     lib.sg_exp_probe.restype = c_i32
     lib.sg_exp_probe.argtypes = [c_void_p, c_void_p, c_i64, c_void_p]
+    version = lib.sg_abi_version()
+    if version != SG_ABI_VERSION:
+        raise RuntimeError(f"ABI mismatch: the library is version {version}, the binding "
+                           f"version {SG_ABI_VERSION}; rebuild with `python -m "
+                           f"specgrove_amd.build`")
     expected = {0: SgTreeAttnArgs, 1: SgKvCommitArgs, 2: SgTreeSampleArgs}
     for which, struct in expected.items():
         size = lib.sg_abi_struct_size(which)

@@ -59,6 +59,7 @@ constexpr int kMaxTreeRows = 256;
 constexpr int kAncWords = kMaxTreeRows / 32;
 constexpr int kMergeThreads = 256;
 constexpr int32_t kPlanMagic = 0x53475041;  // "SGPA"
+constexpr int kMaxGroup = 16;               // query heads per kv head
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazyLog2 = 8.0f;  // softmax reference point moves after a 2^8 growth
 constexpr int kDefaultCUs = 256;
@@ -74,7 +75,12 @@ struct PlanHeader {
   int32_t group;
   int32_t num_partials;
   int32_t num_bins;       // work lists = workgroups of the attention kernel
-  int32_t reserved[8];
+  int32_t num_requests;   // n and R = row_offset[n] of the wave the plan was built for
+  int32_t num_rows;
+  int32_t num_kv_heads;
+  int32_t reserved0;
+  uint64_t meta_hash;     // FNV-1a over row_offset[0..n] and prefix_len[0..n-1]
+  int32_t reserved[2];
 };
 static_assert(sizeof(PlanHeader) == 64, "plan header is 64 bytes");
 
@@ -105,6 +111,22 @@ struct MergeGroup {
   int32_t pad0;
   int32_t pad1;
 };
+
+// 64-bit FNV-1a of the wave's row offsets and prefix lengths (host only).
+uint64_t meta_hash(int n, const int32_t* row_offset, const int32_t* prefix_len) {
+  uint64_t h = 1469598103934665603ull;
+  auto mix = [&](int32_t v) {
+    const uint32_t u = static_cast<uint32_t>(v);
+    for (int b = 0; b < 4; ++b) {
+      h ^= (u >> (8 * b)) & 0xffu;
+      h *= 1099511628211ull;
+    }
+  };
+  mix(n);
+  for (int i = 0; i <= n; ++i) mix(row_offset[i]);
+  for (int i = 0; i < n; ++i) mix(prefix_len[i]);
+  return h;
+}
 
 __host__ __device__ constexpr size_t partial_floats(int head_dim) {
   return static_cast<size_t>(kQPerUnit) * (head_dim + 2);
@@ -213,6 +235,42 @@ struct WaveState {
   floatx16 acc[D / 32];
 };
 
+// The unit's rows and key range lie inside request req's rows and cached
+// prefix as the metadata of this call gives them, and the unit that covers
+// the tree rows ends the key range exactly at the prefix length.
+__device__ __forceinline__ bool unit_matches(const SgTreeAttnArgs& a, const AttnUnit& u, int r0,
+                                             int n, int prefix_len) {
+  return r0 >= 0 && n >= 1 && n <= kMaxTreeRows && r0 <= a.num_rows - n && u.row_begin >= 0 &&
+         u.row_count >= 1 && u.row_begin + u.row_count <= n && u.key_begin >= 0 &&
+         u.key_begin <= u.key_end && u.key_end <= prefix_len &&
+         ((u.flags & 1) == 0 || u.key_end == prefix_len);
+}
+
+// Marks a mismatched unit: the status word, and NaN in its output rows (or in
+// its split partial, which the merge then turns into NaN output).
+template <int D>
+__device__ void poison_unit(const SgTreeAttnArgs& a, const AttnUnit& u, int r0) {
+  const int tid = threadIdx.x;
+  if (tid == 0 && a.status_dev != nullptr) *a.status_dev = SG_EINVAL;
+  const float qnan = __builtin_nanf("");
+  if (u.partial >= 0) {
+    float* part = static_cast<float*>(a.workspace_dev) + partial_floats(D) * u.partial;
+    for (int k = tid; k < static_cast<int>(partial_floats(D)); k += kThreads)
+      part[k] = (k >= kQPerUnit * D && k < kQPerUnit * (D + 1)) ? 0.0f : qnan;
+    return;
+  }
+  const int G = a.num_q_heads / a.num_kv_heads;
+  uint16_t* out = static_cast<uint16_t*>(a.out_dev);
+  for (int k = tid; k < u.row_count * G * D; k += kThreads) {
+    const int rr = k / (G * D);
+    const int h = (k / D) % G;
+    const int64_t row = static_cast<int64_t>(r0) + u.row_begin + rr;
+    if (r0 < 0 || row < 0 || row >= a.num_rows) continue;
+    out[row * a.out_row_stride + static_cast<int64_t>(u.kv_head * G + h) * a.out_head_stride +
+        k % D] = 0x7fc0;  // bf16 quiet NaN
+  }
+}
+
 // Attention of one work unit by the whole workgroup.
 template <int D>
 __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUnit& u) {
@@ -258,9 +316,13 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
   const int head = u.kv_head * G + (m - r_local * G);
   const bool q_valid = active && r_local < u.row_count;
   const int r0 = a.row_offset_dev[u.req];
-  // The planner bounds tree sizes; clamping keeps a mismatched device row_offset
-  // inside the LDS tables.
-  const int n = min(a.row_offset_dev[u.req + 1] - r0, kMaxTreeRows);
+  const int n = a.row_offset_dev[u.req + 1] - r0;
+  // A unit of a plan built for another wave (other prefix lengths or rows)
+  // reads nothing and marks its output instead.
+  if (!unit_matches(a, u, r0, n, a.prefix_len_dev[u.req])) {
+    poison_unit<D>(a, u, r0);
+    return;
+  }
   const int64_t row = static_cast<int64_t>(r0) + u.row_begin + r_local;
   const int g = u.kv_head;
   const bool do_tree = (u.flags & 1) != 0;
@@ -878,6 +940,7 @@ __global__ __launch_bounds__(kMergeThreads) void tree_attn_merge_kernel(SgTreeAt
     const int q4 = (ch / 2) & 3;
     const int hf = ch & 1;
     const int64_t row = static_cast<int64_t>(r0) + grp.row_begin + r_local;
+    if (r0 < 0 || row >= a.num_rows) return;  // metadata of another wave
     uint16_t* dst = static_cast<uint16_t*>(a.out_dev) + row * a.out_row_stride +
                     static_cast<int64_t>(head) * a.out_head_stride + 32 * db + 8 * q4 + 4 * hf;
     uint2 packed;
@@ -905,7 +968,8 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
                  num_q_heads % num_kv_heads == 0,
              "num_q_heads must be a positive multiple of num_kv_heads");
   const int G = num_q_heads / num_kv_heads;
-  SG_REQUIRE(kQPerUnit % G == 0, "query heads per kv head must divide 128");
+  SG_REQUIRE(G <= kMaxGroup && kQPerUnit % G == 0,
+             "query heads per kv head must be 1, 2, 4, 8 or 16");
   SG_REQUIRE(head_dim == 64 || head_dim == 128, "head_dim must be 64 or 128");
   SG_REQUIRE(plan_bytes && plan_units && plan_merges && workspace_bytes, "null output pointer");
   const int rows_per_tile = kQPerUnit / G;
@@ -1119,6 +1183,10 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
   hdr.group = G;
   hdr.num_partials = partials;
   hdr.num_bins = static_cast<int32_t>(lists);
+  hdr.num_requests = num_requests;
+  hdr.num_rows = num_requests > 0 ? row_offset_host[num_requests] : 0;
+  hdr.num_kv_heads = num_kv_heads;
+  hdr.meta_hash = meta_hash(num_requests, row_offset_host, prefix_len_host);
   char* out = static_cast<char*>(plan_host);
   std::memcpy(out, &hdr, sizeof(hdr));
   AttnUnit* uo = reinterpret_cast<AttnUnit*>(out + sizeof(hdr));
@@ -1134,20 +1202,57 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
   return SG_OK;
 }
 
+extern "C" int sg_tree_attn_plan_check(const void* plan_host, int32_t num_requests,
+                                       const int32_t* row_offset_host,
+                                       const int32_t* prefix_len_host) {
+  using namespace sg;
+  clear_error();
+  SG_REQUIRE(plan_host != nullptr, "null plan");
+  SG_REQUIRE(num_requests >= 0, "num_requests must be non-negative");
+  SG_REQUIRE(num_requests == 0 || (row_offset_host && prefix_len_host), "null host array");
+  PlanHeader hdr;
+  std::memcpy(&hdr, plan_host, sizeof(hdr));
+  SG_REQUIRE(hdr.magic == kPlanMagic, "not a plan of sg_tree_attn_plan");
+  SG_REQUIRE(hdr.num_requests == num_requests &&
+                 hdr.meta_hash == meta_hash(num_requests, row_offset_host, prefix_len_host),
+             "the plan was built for another wave (row offsets or prefix lengths differ)");
+  return SG_OK;
+}
+
 extern "C" int sg_tree_attn_fwd(const SgTreeAttnArgs* args, sg_stream_t stream) {
   using namespace sg;
   clear_error();
   SG_REQUIRE(args != nullptr, "null SgTreeAttnArgs");
   const SgTreeAttnArgs& a = *args;
-  SG_REQUIRE(a.num_kv_heads >= 1 && a.num_q_heads % a.num_kv_heads == 0 &&
-                 kQPerUnit % (a.num_q_heads / a.num_kv_heads) == 0,
-             "invalid head configuration");
+  SG_REQUIRE(a.num_kv_heads >= 1 && a.num_q_heads >= a.num_kv_heads &&
+                 a.num_q_heads % a.num_kv_heads == 0,
+             "num_q_heads must be a positive multiple of num_kv_heads");
+  const int G = a.num_q_heads / a.num_kv_heads;
+  SG_REQUIRE(G <= kMaxGroup && kQPerUnit % G == 0,
+             "query heads per kv head must be 1, 2, 4, 8 or 16");
   SG_REQUIRE(a.head_dim == 64 || a.head_dim == 128, "head_dim must be 64 or 128");
+  SG_REQUIRE(a.num_requests >= 0 && a.num_rows >= 0, "negative sizes");
   SG_REQUIRE(a.plan_units >= 0 && a.plan_merges >= 0, "negative plan sizes");
+  if (a.plan_host != nullptr) {
+    PlanHeader hdr;
+    std::memcpy(&hdr, a.plan_host, sizeof(hdr));
+    SG_REQUIRE(hdr.magic == kPlanMagic, "plan_host is not a plan of sg_tree_attn_plan");
+    SG_REQUIRE(hdr.group == G && hdr.head_dim == a.head_dim &&
+                   hdr.num_kv_heads == a.num_kv_heads,
+               "the plan was built for another head configuration");
+    SG_REQUIRE(hdr.num_requests == a.num_requests && hdr.num_rows == a.num_rows,
+               "the plan was built for another wave (request or row count differs)");
+    SG_REQUIRE(hdr.num_bins == a.plan_units && hdr.num_merges == a.plan_merges,
+               "plan_units / plan_merges disagree with the plan");
+    SG_REQUIRE(a.plan_merges == 0 ||
+                   a.workspace_bytes >= sizeof(float) * partial_floats(a.head_dim) *
+                                            static_cast<size_t>(hdr.num_partials),
+               "workspace below the plan's split partials");
+  }
   if (a.plan_units == 0) return SG_OK;
   SG_REQUIRE(a.q_dev && a.k_cache_dev && a.v_cache_dev && a.k_tree_dev && a.v_tree_dev &&
-                 a.row_offset_dev && a.prefix_start_dev && a.parent_dev && a.out_dev &&
-                 a.plan_dev,
+                 a.row_offset_dev && a.prefix_start_dev && a.prefix_len_dev && a.parent_dev &&
+                 a.out_dev && a.plan_dev,
              "null device pointer");
   SG_REQUIRE(a.plan_merges == 0 || a.workspace_dev, "split plan needs a workspace");
   SG_REQUIRE(a.q_row_stride % 8 == 0 && a.q_head_stride % 8 == 0 &&

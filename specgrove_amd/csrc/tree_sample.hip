@@ -27,6 +27,9 @@
 
 #include <limits.h>
 
+#include <string>
+#include <type_traits>
+
 #include "sg_common.h"
 
 namespace sg {
@@ -124,35 +127,62 @@ __device__ __forceinline__ float wave_butterfly_sum(float v) {
 }
 
 typedef __attribute__((ext_vector_type(4))) float floatx4;
+typedef __attribute__((ext_vector_type(2))) unsigned int uintx2;
+
+// Logits element types.  bf16 and f16 widen to fp32 exactly, so a row of
+// either type gives the same statistics and decisions as its fp32 copy.
+struct Bf16 {
+  uint16_t bits;
+};
+struct F16 {
+  _Float16 v;
+};
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(Bf16 v) { return bf16_to_f32(v.bits); }
+__device__ __forceinline__ float to_f32(F16 v) { return static_cast<float>(v.v); }
+
+template <typename S>
+__device__ __forceinline__ S half_at(uint32_t word, int hi) {
+  return __builtin_bit_cast(S, static_cast<uint16_t>(hi ? (word >> 16) : (word & 0xffffu)));
+}
+
+// Four consecutive elements at p (16-byte aligned for fp32, 8-byte for the
+// 16-bit types), widened to fp32.
+template <typename S, bool kStream>
+__device__ __forceinline__ void load4(const S* __restrict__ p, float out[4]) {
+  if constexpr (sizeof(S) == 4) {
+    const floatx4 q = kStream ? __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(p))
+                              : *reinterpret_cast<const floatx4*>(p);
+    out[0] = q[0];
+    out[1] = q[1];
+    out[2] = q[2];
+    out[3] = q[3];
+  } else {
+    const uintx2 q = kStream ? __builtin_nontemporal_load(reinterpret_cast<const uintx2*>(p))
+                             : *reinterpret_cast<const uintx2*>(p);
+    out[0] = to_f32(half_at<S>(q[0], 0));
+    out[1] = to_f32(half_at<S>(q[0], 1));
+    out[2] = to_f32(half_at<S>(q[1], 0));
+    out[3] = to_f32(half_at<S>(q[1], 1));
+  }
+}
 
 // Lane l of the wave loads tokens 2048*s + 256*j + 4*l + c into v[4*j + c];
 // tokens at or beyond vocab read as -inf (they contribute E = 0).
-template <bool kVec4, bool kStream = false>
-__device__ __forceinline__ void load_slab(const float* __restrict__ x, int vocab,
+template <typename S, bool kVec, bool kStream = false>
+__device__ __forceinline__ void load_slab(const S* __restrict__ x, int vocab,
                                           int slab, int lane, float v[32]) {
   const int base = slab * kSlab + 4 * lane;
-  if (kVec4 && (slab + 1) * kSlab <= vocab) {  // full slab: no bounds checks
+  if (kVec && (slab + 1) * kSlab <= vocab) {  // full slab: no bounds checks
+    // Non-temporal when asked: the statistics pass reads every row once.
 #pragma unroll
-    for (int j = 0; j < kLinesPerSlab; ++j) {
-      // Non-temporal: the statistics pass reads every row once.
-      const floatx4 q =
-          kStream ? __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(x + base + kLine * j))
-                  : *reinterpret_cast<const floatx4*>(x + base + kLine * j);
-      v[4 * j + 0] = q[0];
-      v[4 * j + 1] = q[1];
-      v[4 * j + 2] = q[2];
-      v[4 * j + 3] = q[3];
-    }
-  } else if (kVec4) {
+    for (int j = 0; j < kLinesPerSlab; ++j) load4<S, kStream>(x + base + kLine * j, v + 4 * j);
+  } else if (kVec) {
 #pragma unroll
     for (int j = 0; j < kLinesPerSlab; ++j) {
       const int t = base + kLine * j;
       if (t < vocab) {
-        const float4 q = *reinterpret_cast<const float4*>(x + t);
-        v[4 * j + 0] = q.x;
-        v[4 * j + 1] = q.y;
-        v[4 * j + 2] = q.z;
-        v[4 * j + 3] = q.w;
+        load4<S, false>(x + t, v + 4 * j);
       } else {
         v[4 * j + 0] = v[4 * j + 1] = v[4 * j + 2] = v[4 * j + 3] = -__builtin_inff();
       }
@@ -163,7 +193,7 @@ __device__ __forceinline__ void load_slab(const float* __restrict__ x, int vocab
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int t = base + kLine * j + c;
-        v[4 * j + c] = (t < vocab) ? x[t] : -__builtin_inff();
+        v[4 * j + c] = (t < vocab) ? to_f32(x[t]) : -__builtin_inff();
       }
     }
   }
@@ -200,25 +230,28 @@ __device__ __forceinline__ MZ slab_stats(const float v[32]) {
 // faster over the whole sampling call than five 4-wave workgroups per CU
 // (102 VGPRs), and equal to a grid that gives every workgroup the same
 // number of (row, slab) tasks.
-template <bool kVec4>
+// Workgroup 0 also clears the caller's status word (when given): the later
+// kernels of the call only ever raise it.
+template <typename S, bool kVec>
 __global__ __launch_bounds__(kStatsThreads, 2) void row_stats_kernel(
-    const float* __restrict__ logits, int64_t row_stride, int vocab, int rows,
-    float* __restrict__ row_max, float* __restrict__ row_sum) {
+    const S* __restrict__ logits, int64_t row_stride, int vocab, int rows,
+    float* __restrict__ row_max, float* __restrict__ row_sum, int32_t* __restrict__ status) {
   __shared__ float s_m[kMaxSlabs];
   __shared__ float s_z[kMaxSlabs];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int row = blockIdx.x;
+  if (row == 0 && threadIdx.x == 0 && status != nullptr) *status = SG_OK;
   if (row >= rows) return;
-  const float* __restrict__ x = logits + row_stride * row;
+  const S* __restrict__ x = logits + row_stride * row;
   const int slabs = (vocab + kSlab - 1) / kSlab;
   constexpr int kWavesPerRow = kStatsThreads / kWave;
   float v[32], w[32];
   int s = wave;
-  if (s < slabs) load_slab<kVec4, true>(x, vocab, s, lane, v);
+  if (s < slabs) load_slab<S, kVec, true>(x, vocab, s, lane, v);
   while (s < slabs) {
     const int next = s + kWavesPerRow;
-    if (next < slabs) load_slab<kVec4, true>(x, vocab, next, lane, w);
+    if (next < slabs) load_slab<S, kVec, true>(x, vocab, next, lane, w);
     const MZ a = slab_stats(v);
     if (lane == 0) {
       s_m[s] = a.m;
@@ -226,7 +259,7 @@ __global__ __launch_bounds__(kStatsThreads, 2) void row_stats_kernel(
     }
     if (next >= slabs) break;
     const int next2 = next + kWavesPerRow;
-    if (next2 < slabs) load_slab<kVec4, true>(x, vocab, next2, lane, v);
+    if (next2 < slabs) load_slab<S, kVec, true>(x, vocab, next2, lane, v);
     const MZ b = slab_stats(w);
     if (lane == 0) {
       s_m[next] = b.m;
@@ -269,11 +302,11 @@ __device__ __forceinline__ uint32_t child_bits(const int* child_tok, int count,
 }
 
 // Exit-row values of one slab: e = 0 for child tokens and tokens >= vocab.
-template <bool kVec4>
-__device__ __forceinline__ void exit_values(const float* __restrict__ x, int vocab,
+template <typename S, bool kVec>
+__device__ __forceinline__ void exit_values(const S* __restrict__ x, int vocab,
                                             float m, int slab, int lane,
                                             uint32_t bits, float e[32]) {
-  load_slab<kVec4>(x, vocab, slab, lane, e);
+  load_slab<S, kVec>(x, vocab, slab, lane, e);
 #pragma unroll
   for (int k = 0; k < 32; ++k) {
     const float val = sg_exp_nonpos(e[k] - m);
@@ -320,8 +353,10 @@ struct RouteShared {
 // the children in ascending node order accumulate S += E(x_v[token] - m_v) and
 // the first child with u[2d] * Z_v < S is accepted.  Accepted nodes are
 // written to nodes_out when write_nodes.  Ends with a barrier.
+template <typename S>
 __device__ void route_request(const SgTreeSampleArgs& a, int req, int r0, int n,
                               RouteShared& sh, bool write_nodes) {
+  const S* __restrict__ logits = static_cast<const S*>(a.logits_dev);
   const int tid = threadIdx.x;
   const float* __restrict__ u = a.uniforms_dev + static_cast<int64_t>(a.uniform_stride) * req;
   const int n_u = min(a.uniform_stride, 2 * kMaxTreeRows + 2);
@@ -333,7 +368,7 @@ __device__ void route_request(const SgTreeSampleArgs& a, int req, int r0, int n,
     sh.rm[k] = a.row_max_dev[r0 + k];
     sh.rz[k] = a.row_sum_dev[r0 + k];
     const bool readable = k > 0 && p >= 0 && p < k && tok >= 0 && tok < a.vocab;
-    sh.xchild[k] = readable ? a.logits_dev[a.logits_row_stride * (r0 + p) + tok] : 0.0f;
+    sh.xchild[k] = readable ? to_f32(logits[a.logits_row_stride * (r0 + p) + tok]) : 0.0f;
   }
   for (int k = tid; k < n_u; k += blockDim.x) sh.u[k] = u[k];
   __syncthreads();
@@ -408,7 +443,7 @@ __device__ void route_request(const SgTreeSampleArgs& a, int req, int r0, int n,
 //   ((e0+e1)+e2)+e3; inclusive Kogge-Stone scan over the 64 lanes of a line;
 //   slab total = sequential sum of the line totals.  The line totals are kept
 //   too, for part 2.
-template <bool kVec4>
+template <typename S, bool kVec>
 __global__ __launch_bounds__(kWalkThreads) void exit_totals_kernel(SgTreeSampleArgs a) {
   __shared__ RouteShared sh;
   const int req = blockIdx.x;
@@ -418,7 +453,9 @@ __global__ __launch_bounds__(kWalkThreads) void exit_totals_kernel(SgTreeSampleA
   const int wave = tid / kWave;
   const int r0 = a.row_offset_dev[req];
   const int n = a.row_offset_dev[req + 1] - r0;
-  if (n < 1 || n > kMaxTreeRows) {
+  // A request must own 1 to kMaxTreeRows rows inside the num_rows rows whose
+  // statistics were computed; the walk reports any other as a broken contract.
+  if (n < 1 || n > kMaxTreeRows || r0 < 0 || r0 > a.num_rows - n) {
     if (chunk == 0 && tid == 0) {
       a.accept_len_dev[req] = -1;
       a.bonus_dev[req] = -1;
@@ -430,7 +467,7 @@ __global__ __launch_bounds__(kWalkThreads) void exit_totals_kernel(SgTreeSampleA
   if (chunk == 0)
     for (int k = tid; k < a.max_depth; k += blockDim.x) nodes_out[k] = -1;
   __syncthreads();
-  route_request(a, req, r0, n, sh, chunk == 0);
+  route_request<S>(a, req, r0, n, sh, chunk == 0);
   if (chunk == 0) {
     if (tid == 0) {
       a.accept_len_dev[req] = sh.broken ? -1 : sh.depth;
@@ -463,10 +500,10 @@ __global__ __launch_bounds__(kWalkThreads) void exit_totals_kernel(SgTreeSampleA
   const int s = chunk * kWalkWaves + wave;
   if (s >= slabs) return;
   const int64_t row = r0 + sh.exit_node;
-  const float* __restrict__ x = a.logits_dev + a.logits_row_stride * row;
+  const S* __restrict__ x = static_cast<const S*>(a.logits_dev) + a.logits_row_stride * row;
   const float m = sh.rm[sh.exit_node];
   float e[32], incl[kLinesPerSlab], total[kLinesPerSlab];
-  exit_values<kVec4>(x, a.vocab, m, s, lane, child_bits(sh.child_tok, sh.child_count, s, lane),
+  exit_values<S, kVec>(x, a.vocab, m, s, lane, child_bits(sh.child_tok, sh.child_count, s, lane),
                      e);
   line_scans(e, lane, incl, total);
   float lp = 0.0f;
@@ -491,7 +528,7 @@ __global__ __launch_bounds__(kWalkThreads) void exit_totals_kernel(SgTreeSampleA
 // threshold - 1e-4 * C cannot hold that token (its running values differ from
 // that sum by a few roundings), so only the lines from the first one that may
 // are recomputed, one 256-token line at a time.
-template <bool kVec4>
+template <typename S, bool kVec>
 __global__ __launch_bounds__(kWave) void exit_find_kernel(SgTreeSampleArgs a) {
   __shared__ int s_child_tok[kMaxTreeRows];
   __shared__ float s_total[kMaxSlabs];
@@ -521,7 +558,7 @@ __global__ __launch_bounds__(kWave) void exit_find_kernel(SgTreeSampleArgs a) {
   for (int q = 0; q < (kMaxSlabs + kWave - 1) / kWave; ++q)
     tot[q] = q * kWave + lane < slabs ? totals[q * kWave + lane] : 0.0f;
   // The record exists only for a valid tree; part 1 reported the others.
-  if (n < 1 || n > kMaxTreeRows) return;
+  if (n < 1 || n > kMaxTreeRows || r0 < 0 || r0 > a.num_rows - n) return;
   if (depth < 0) return;  // broken walk, reported by part 1
   if (lane < count) s_child_tok[lane] = tok0;
   for (int k = kWave + lane; k < count; k += kWave) s_child_tok[k] = rec[4 + k];
@@ -579,21 +616,18 @@ __global__ __launch_bounds__(kWave) void exit_find_kernel(SgTreeSampleArgs a) {
       ++j;
     }
   }
-  const float* __restrict__ x = a.logits_dev + a.logits_row_stride * row;
+  const S* __restrict__ x = static_cast<const S*>(a.logits_dev) + a.logits_row_stride * row;
   int candidate = INT_MAX;
   while (s < slabs && candidate == INT_MAX) {
     // Line j of slab s: lane l holds tokens 2048*s + 256*j + 4*l + c.
     const int t0 = s * kSlab + kLine * j + 4 * lane;
     float e[4];
-    if (kVec4 && t0 + 3 < a.vocab) {
-      const float4 q = *reinterpret_cast<const float4*>(x + t0);
-      e[0] = q.x;
-      e[1] = q.y;
-      e[2] = q.z;
-      e[3] = q.w;
+    if (kVec && t0 + 3 < a.vocab) {
+      load4<S, false>(x + t0, e);
     } else {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) e[c] = (t0 + c < a.vocab) ? x[t0 + c] : -__builtin_inff();
+      for (int c = 0; c < 4; ++c)
+        e[c] = (t0 + c < a.vocab) ? to_f32(x[t0 + c]) : -__builtin_inff();
     }
     const uint32_t bits = child_bits(s_child_tok, count, s, lane) >> (4 * j);
 #pragma unroll
@@ -651,21 +685,38 @@ __global__ void exp_probe_kernel(const float* __restrict__ x, float* __restrict_
   if (k < count) out[k] = sg_exp(x[k]);
 }
 
-bool vec4_ok(const float* p, int64_t stride, int vocab) {
-  return (reinterpret_cast<uintptr_t>(p) % 16 == 0) && stride % 4 == 0 && vocab % 4 == 0;
+size_t elem_bytes(int dtype) { return dtype == SG_DTYPE_F32 ? 4 : 2; }
+
+// Whole 4-element groups (16 bytes of fp32, 8 bytes of bf16/f16) are aligned.
+bool vec_ok(const void* p, int dtype, int64_t stride, int vocab) {
+  return (reinterpret_cast<uintptr_t>(p) % (4 * elem_bytes(dtype)) == 0) && stride % 4 == 0 &&
+         vocab % 4 == 0;
 }
 
-int launch_row_stats(const float* logits, int64_t stride, int vocab, int rows,
-                     float* row_max, float* row_sum, hipStream_t stream) {
-  if (rows == 0) return SG_OK;
-  const dim3 grid(rows);  // one workgroup per row
-  if (vec4_ok(logits, stride, vocab)) {
-    hipLaunchKernelGGL(row_stats_kernel<true>, grid, dim3(kStatsThreads), 0, stream,
-                       logits, stride, vocab, rows, row_max, row_sum);
+// Calls f(S{}, BoolTag) with the element type and vector flag of the logits.
+template <typename F>
+void dispatch_logits(const void* p, int dtype, int64_t stride, int vocab, F&& f) {
+  const bool vec = vec_ok(p, dtype, stride, vocab);
+  if (dtype == SG_DTYPE_BF16) {
+    vec ? f(Bf16{}, std::true_type{}) : f(Bf16{}, std::false_type{});
+  } else if (dtype == SG_DTYPE_F16) {
+    vec ? f(F16{}, std::true_type{}) : f(F16{}, std::false_type{});
   } else {
-    hipLaunchKernelGGL(row_stats_kernel<false>, grid, dim3(kStatsThreads), 0, stream,
-                       logits, stride, vocab, rows, row_max, row_sum);
+    vec ? f(float{}, std::true_type{}) : f(float{}, std::false_type{});
   }
+}
+
+int launch_row_stats(const void* logits, int dtype, int64_t stride, int vocab, int rows,
+                     float* row_max, float* row_sum, int32_t* status, hipStream_t stream) {
+  if (rows == 0 && status == nullptr) return SG_OK;
+  // One workgroup per row (one to clear the status when there are no rows).
+  const dim3 grid(rows > 0 ? rows : 1);
+  dispatch_logits(logits, dtype, stride, vocab, [&](auto elem, auto vec) {
+    using S = decltype(elem);
+    hipLaunchKernelGGL((row_stats_kernel<S, decltype(vec)::value>), grid, dim3(kStatsThreads),
+                       0, stream, static_cast<const S*>(logits), stride, vocab, rows, row_max,
+                       row_sum, status);
+  });
   SG_LAUNCH_CHECK();
   return SG_OK;
 }
@@ -673,18 +724,21 @@ int launch_row_stats(const float* logits, int64_t stride, int vocab, int rows,
 }  // namespace
 }  // namespace sg
 
-extern "C" int sg_row_stats(const float* logits_dev, int64_t row_stride, int32_t vocab,
-                            int32_t num_rows, float* row_max_dev, float* row_sum_dev,
-                            sg_stream_t stream) {
+extern "C" int sg_row_stats(const void* logits_dev, int32_t logits_dtype, int64_t row_stride,
+                            int32_t vocab, int32_t num_rows, float* row_max_dev,
+                            float* row_sum_dev, sg_stream_t stream) {
   using namespace sg;
   clear_error();
+  SG_REQUIRE(logits_dtype == SG_DTYPE_F32 || logits_dtype == SG_DTYPE_BF16 ||
+                 logits_dtype == SG_DTYPE_F16,
+             "logits_dtype must be SG_DTYPE_F32, SG_DTYPE_BF16 or SG_DTYPE_F16");
   SG_REQUIRE(vocab >= 1 && vocab <= kMaxSlabs * kSlab, "vocab must be in [1, 524288]");
   SG_REQUIRE(num_rows >= 0, "num_rows must be non-negative");
   SG_REQUIRE(row_stride >= vocab, "logits row stride is below the vocabulary");
   SG_REQUIRE(num_rows == 0 || (logits_dev && row_max_dev && row_sum_dev),
              "null device pointer");
-  return launch_row_stats(logits_dev, row_stride, vocab, num_rows, row_max_dev,
-                          row_sum_dev, reinterpret_cast<hipStream_t>(stream));
+  return launch_row_stats(logits_dev, logits_dtype, row_stride, vocab, num_rows, row_max_dev,
+                          row_sum_dev, nullptr, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int64_t sg_tree_sample_workspace_bytes(int32_t num_requests, int32_t vocab) {
@@ -705,6 +759,9 @@ int check_sample_args(const SgTreeSampleArgs* args) {
   SG_REQUIRE(args != nullptr, "null SgTreeSampleArgs");
   const SgTreeSampleArgs& a = *args;
   SG_REQUIRE(a.num_requests >= 0 && a.num_rows >= 0, "negative sizes");
+  SG_REQUIRE(a.logits_dtype == SG_DTYPE_F32 || a.logits_dtype == SG_DTYPE_BF16 ||
+                 a.logits_dtype == SG_DTYPE_F16,
+             "logits_dtype must be SG_DTYPE_F32, SG_DTYPE_BF16 or SG_DTYPE_F16");
   SG_REQUIRE(a.vocab >= 1 && a.vocab <= kMaxSlabs * kSlab, "vocab must be in [1, 524288]");
   SG_REQUIRE(a.logits_row_stride >= a.vocab, "logits row stride is below the vocabulary");
   SG_REQUIRE(a.max_depth >= 0, "max_depth must be non-negative");
@@ -721,22 +778,24 @@ int check_sample_args(const SgTreeSampleArgs* args) {
 // Enqueues the three kernels of one sampling call; a.workspace_dev holds at
 // least sg_tree_sample_workspace_bytes(num_requests, vocab) bytes.
 int launch_tree_sample(const SgTreeSampleArgs& a, hipStream_t s) {
-  int rc = launch_row_stats(a.logits_dev, a.logits_row_stride, a.vocab, a.num_rows,
-                            a.row_max_dev, a.row_sum_dev, s);
+  int rc = launch_row_stats(a.logits_dev, a.logits_dtype, a.logits_row_stride, a.vocab,
+                            a.num_rows, a.row_max_dev, a.row_sum_dev, a.status_dev, s);
   if (rc != SG_OK) return rc;
   const int slabs = (a.vocab + kSlab - 1) / kSlab;
   const dim3 grid1(a.num_requests, (slabs + kWalkWaves - 1) / kWalkWaves);
-  if (vec4_ok(a.logits_dev, a.logits_row_stride, a.vocab)) {
-    hipLaunchKernelGGL(exit_totals_kernel<true>, grid1, dim3(kWalkThreads), 0, s, a);
-    SG_LAUNCH_CHECK();
-    hipLaunchKernelGGL(exit_find_kernel<true>, dim3(a.num_requests), dim3(kWave), 0, s,
-                       a);
-  } else {
-    hipLaunchKernelGGL(exit_totals_kernel<false>, grid1, dim3(kWalkThreads), 0, s, a);
-    SG_LAUNCH_CHECK();
-    hipLaunchKernelGGL(exit_find_kernel<false>, dim3(a.num_requests), dim3(kWave), 0, s,
-                       a);
-  }
+  hipError_t err = hipSuccess;
+  dispatch_logits(a.logits_dev, a.logits_dtype, a.logits_row_stride, a.vocab,
+                  [&](auto elem, auto vec) {
+                    using S = decltype(elem);
+                    constexpr bool kVec = decltype(vec)::value;
+                    hipLaunchKernelGGL((exit_totals_kernel<S, kVec>), grid1, dim3(kWalkThreads),
+                                       0, s, a);
+                    err = hipGetLastError();
+                    if (err != hipSuccess) return;
+                    hipLaunchKernelGGL((exit_find_kernel<S, kVec>), dim3(a.num_requests),
+                                       dim3(kWave), 0, s, a);
+                  });
+  SG_HIP_CHECK(err);
   SG_LAUNCH_CHECK();
   return SG_OK;
 }

@@ -58,6 +58,19 @@ class AttnPlan:
     device: torch.Tensor | None = None
     workspace: torch.Tensor | None = None
 
+    @property
+    def header(self) -> np.ndarray:
+        """The plan header as int32 words (see decode_plan)."""
+        return self.host[:64].view(np.int32)
+
+    @property
+    def num_requests(self) -> int:
+        return int(self.header[8])
+
+    @property
+    def num_rows(self) -> int:
+        return int(self.header[9])
+
     def to(self, device) -> "AttnPlan":
         """Copy the plan to the device and allocate its workspace (the fp32
         partial results of split units; every slot is written before the merge
@@ -94,6 +107,30 @@ def plan_attention(row_offset, prefix_len, num_q_heads: int, num_kv_heads: int,
                     num_kv_heads, head_dim)
 
 
+def check_plan(plan: AttnPlan, row_offset_host, prefix_len_host) -> None:
+    """Raise ValueError unless ``plan`` was built from exactly these row
+    offsets and prefix lengths (plans are per wave: prefix lengths change
+    after every commit)."""
+    ro = np.ascontiguousarray(np.asarray(row_offset_host, dtype=np.int32))
+    pl = np.ascontiguousarray(np.asarray(prefix_len_host, dtype=np.int32))
+    _require(ro.size == pl.size + 1, "row_offset must have num_requests + 1 entries")
+    i32p = ctypes.POINTER(ctypes.c_int32)
+    _lib.check(_lib.load().sg_tree_attn_plan_check(
+        plan.host.ctypes.data_as(ctypes.c_void_p), int(pl.size), ro.ctypes.data_as(i32p),
+        pl.ctypes.data_as(i32p)), "sg_tree_attn_plan_check")
+
+
+def check_plan_call(plan: AttnPlan, num_requests: int, num_rows: int, num_q_heads: int,
+                    num_kv_heads: int, head_dim: int) -> None:
+    """Host-side agreement of a plan with the call's shapes (no device access)."""
+    _require((plan.num_q_heads, plan.num_kv_heads, plan.head_dim)
+             == (num_q_heads, num_kv_heads, head_dim),
+             "plan was built for another head configuration")
+    _require(plan.num_requests == num_requests and plan.num_rows == num_rows,
+             f"plan was built for another wave ({plan.num_requests} requests, "
+             f"{plan.num_rows} rows; the call has {num_requests} and {num_rows})")
+
+
 UNIT_FIELDS = ("req", "kv_head", "row_begin", "row_count", "key_begin", "key_end",
                "partial", "flags", "group", "num_splits", "first_partial", "pad")
 
@@ -123,13 +160,16 @@ def tree_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor
                    row_offset: torch.Tensor, prefix_start: torch.Tensor,
                    prefix_len: torch.Tensor, parent: torch.Tensor, plan: AttnPlan,
                    out: torch.Tensor | None = None, scale: float | None = None,
-                   ) -> torch.Tensor:
+                   status: torch.Tensor | None = None) -> torch.Tensor:
     """Packed tree attention of one layer.
 
     q [R, Hq, D], k/v_cache [Hkv, tokens, D] (the cache arena of this layer),
     k/v_tree [R, Hkv, D] (this wave's rows), row_offset [n+1] i32,
     prefix_start [n] i64, prefix_len [n] i32, parent [R] i32.  Returns
-    out [R, Hq, D] bf16.
+    out [R, Hq, D] bf16.  ``status`` (optional [1] i32 device word, never
+    cleared here) is set to SG_EINVAL by any unit whose key range or rows
+    disagree with prefix_len / row_offset (a plan of another wave), whose
+    output rows are then NaN.
     """
     for t, name in ((q, "q"), (k_cache, "k_cache"), (v_cache, "v_cache"),
                     (k_tree, "k_tree"), (v_tree, "v_tree")):
@@ -148,13 +188,14 @@ def tree_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor
              and k_tree.stride() == v_tree.stride(),
              "k_tree/v_tree must be [R, Hkv, D] with equal strides")
     _require(k_cache.shape[2] == dim, "head dims disagree")
-    _require((plan.num_q_heads, plan.num_kv_heads, plan.head_dim) == (hq, hkv, dim),
-             "plan was built for another head configuration")
+    n = prefix_len.numel()
+    check_plan_call(plan, n, rows, hq, hkv, dim)
     _require(plan.device is not None and plan.device.is_cuda, "plan is not on the device")
     _require(parent.numel() >= rows, "parent must cover every packed row")
-    n = prefix_len.numel()
     _require(row_offset.numel() == n + 1 and prefix_start.numel() == n,
              "request metadata sizes disagree")
+    if status is not None:
+        _check_device_tensor(status, "status", torch.int32)
     if out is None:
         out = torch.empty((rows, hq, dim), dtype=torch.bfloat16, device=q.device)
     _check_rows(out, "out")
@@ -181,6 +222,8 @@ def tree_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor
     a.out_dev = out.data_ptr()
     a.out_row_stride, a.out_head_stride = out.stride(0), out.stride(1)
     a.plan_dev = plan.device.data_ptr()
+    a.plan_host = plan.host.ctypes.data
+    a.status_dev = status.data_ptr() if status is not None else 0
     a.plan_units = plan.units
     a.plan_merges = plan.merges
     a.workspace_dev = plan.workspace.data_ptr() if plan.workspace is not None else 0
@@ -268,9 +311,41 @@ class SampleResult:
     workspace: torch.Tensor | None = None  # per-slab complement totals of the exit rows
 
 
-def _check_sample_inputs(logits, row_offset, parent, token, uniforms, max_depth):
-    _check_device_tensor(logits, "logits", torch.float32)
+_LOGITS_DTYPES = {torch.float32: _lib.SG_DTYPE_F32, torch.bfloat16: _lib.SG_DTYPE_BF16,
+                  torch.float16: _lib.SG_DTYPE_F16}
+
+
+def _check_logits(logits: torch.Tensor) -> int:
+    _require(isinstance(logits, torch.Tensor) and logits.is_cuda,
+             "logits must be a HIP device tensor")
+    _require(logits.dtype in _LOGITS_DTYPES,
+             f"logits must be float32, bfloat16 or float16, got {logits.dtype}")
     _require(logits.dim() == 2 and logits.stride(1) == 1, "logits must be [R, V] row-contiguous")
+    return _LOGITS_DTYPES[logits.dtype]
+
+
+def _check_sample_out(out: "SampleResult", n: int, rows: int, max_depth: int) -> None:
+    """Caller-supplied outputs must fit this call exactly (the kernels index
+    them by n, R and max_depth)."""
+    expect = {
+        "accept_nodes": ((n, max(max_depth, 1)), torch.int32),
+        "accept_len": ((n,), torch.int32),
+        "bonus": ((n,), torch.int32),
+        "keep_rows": ((n, max_depth + 1), torch.int32),
+        "row_max": ((rows,), torch.float32),
+        "row_sum": ((rows,), torch.float32),
+        "status": ((1,), torch.int32),
+    }
+    for name, (shape, dtype) in expect.items():
+        t = getattr(out, name)
+        _check_device_tensor(t, f"out.{name}", dtype)
+        _require(tuple(t.shape) == shape and t.is_contiguous(),
+                 f"out.{name} must be a contiguous {list(shape)} tensor for this call, "
+                 f"got {list(t.shape)}")
+
+
+def _check_sample_inputs(logits, row_offset, parent, token, uniforms, max_depth):
+    _check_logits(logits)
     for t, name in ((row_offset, "row_offset"), (parent, "parent"), (token, "token")):
         _check_device_tensor(t, name, torch.int32)
         _require(t.is_contiguous(), f"{name} must be contiguous")
@@ -291,6 +366,7 @@ def _sample_args(logits, row_offset, parent, token, uniforms, max_depth, out, n,
     a.num_rows = rows
     a.vocab = logits.shape[1]
     a.max_depth = max_depth
+    a.logits_dtype = _LOGITS_DTYPES[logits.dtype]
     a.logits_dev = logits.data_ptr()
     a.logits_row_stride = logits.stride(0)
     a.row_offset_dev = row_offset.data_ptr()
@@ -315,9 +391,11 @@ def tree_sample(logits: torch.Tensor, row_offset: torch.Tensor, parent: torch.Te
                 out: SampleResult | None = None) -> SampleResult:
     """Temperature-1 tree rejection sampling over all packed rows.
 
-    logits [R, V] fp32 (row-contiguous), row_offset [n+1] i32, parent/token
+    logits [R, V] fp32, bf16 or f16 (row-contiguous; the 16-bit types widen to
+    fp32 exactly), row_offset [n+1] i32 with row_offset[n] == R, parent/token
     [R] i32 (request-local parents, -1 for roots), uniforms [n, U] fp32 with
-    U >= 2*(max_depth+1).
+    U >= 2*(max_depth+1).  ``out`` (optional) must have been made for the same
+    n, R and max_depth; its status word is cleared by the call.
     """
     n, rows = _check_sample_inputs(logits, row_offset, parent, token, uniforms, max_depth)
     dev = logits.device
@@ -332,6 +410,8 @@ def tree_sample(logits: torch.Tensor, row_offset: torch.Tensor, parent: torch.Te
             row_sum=torch.empty(rows, dtype=torch.float32, device=dev),
             status=torch.zeros(1, dtype=torch.int32, device=dev),
         )
+    else:
+        _check_sample_out(out, n, rows, max_depth)
     ws_bytes = int(_lib.load().sg_tree_sample_workspace_bytes(n, logits.shape[1]))
     if out.workspace is None or out.workspace.numel() < ws_bytes:
         out.workspace = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
@@ -349,6 +429,7 @@ def tree_sample_noalloc(logits: torch.Tensor, row_offset: torch.Tensor, parent: 
     the caller supplies every output in ``out`` (its ``workspace`` is unused)."""
     n, rows = _check_sample_inputs(logits, row_offset, parent, token, uniforms, max_depth)
     _require(isinstance(out, SampleResult), "sg_tree_sample_noalloc needs caller-owned outputs")
+    _check_sample_out(out, n, rows, max_depth)
     a = _sample_args(logits, row_offset, parent, token, uniforms, max_depth, out, n, rows, None)
     _lib.check(_lib.load().sg_tree_sample_noalloc(ctypes.byref(a), _stream_handle()),
                "sg_tree_sample_noalloc")
@@ -356,13 +437,13 @@ def tree_sample_noalloc(logits: torch.Tensor, row_offset: torch.Tensor, parent: 
 
 
 def row_stats(logits: torch.Tensor):
-    _check_device_tensor(logits, "logits", torch.float32)
-    _require(logits.dim() == 2 and logits.stride(1) == 1, "logits must be [R, V] row-contiguous")
+    dtype = _check_logits(logits)
     rows = logits.shape[0]
     m = torch.empty(rows, dtype=torch.float32, device=logits.device)
     z = torch.empty(rows, dtype=torch.float32, device=logits.device)
-    _lib.check(_lib.load().sg_row_stats(logits.data_ptr(), logits.stride(0), logits.shape[1],
-                                        rows, m.data_ptr(), z.data_ptr(), _stream_handle()),
+    _lib.check(_lib.load().sg_row_stats(logits.data_ptr(), dtype, logits.stride(0),
+                                        logits.shape[1], rows, m.data_ptr(), z.data_ptr(),
+                                        _stream_handle()),
                "sg_row_stats")
     return m, z
 

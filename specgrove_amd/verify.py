@@ -11,7 +11,7 @@ the whole wave and one device-to-host transfer, and the same
 
 Differences, by design:
 
-* the sampler reads fp32 logits and does its own fp32 softmax with the
+* the sampler reads fp32, bf16 or f16 logits and does its own fp32 softmax with the
   reference's law (sampling.py:903-950): routing by ``u[2d]`` over the
   children's cumulative mass, residual draw by ``u[2d+1]`` over the
   complement of the children (fused_tree_sampling.py:683-824); the
@@ -91,8 +91,12 @@ def tree_verify_hip_rejection_batched(parents_batch: Sequence[Sequence[int]],
     vocab = logits.shape[1]
     if any(token < 0 or token >= vocab for _, tokens, _ in topologies for token in tokens):
         raise ValueError("Tree token is outside the Target vocabulary")
-    if logits.dtype != torch.float32 or logits.stride(1) != 1:
-        logits = logits.float().contiguous()
+    # fp32, bf16 and f16 rows are read as they are (the 16-bit types widen to
+    # fp32 exactly inside the kernels); other types are rounded to fp32.
+    if logits.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        logits = logits.float()
+    if logits.stride(1) != 1 or logits.stride(0) < logits.shape[1]:
+        logits = logits.contiguous()
     if validate and not bool(torch.isfinite(logits).all()):
         raise FloatingPointError("Invalid Target logits for the HIP tree verifier")
 

@@ -13,7 +13,8 @@ Shapes follow the five workloads the path is measured on:
   sampler   64 requests x 32 nodes, vocab 151936, fp32 logits N(0, 3^2) with 1-5
             peaks +12, draft q = 0.7 softmax + 0.3 Dirichlet(0.1);
   long_ctx  128 requests, prefixes log-uniform [8192, 32768], tiers
-            {1,16,32,64,128} weighted {.1,.2,.3,.25,.15}, 4096-row budget.
+            {1,16,32,64,128} weighted {.1,.2,.3,.25,.15}, 4096-row budget;
+  tier128   the qwen3_8b shape with 16 requests all at the 128-node tier.
 
 Row convention: a tier of k nodes is k packed rows including the root (row 0
 of a request block is the newest committed token, as ids = [root] + tokens in
@@ -75,7 +76,16 @@ def depths_of(parents) -> list[int]:
 
 
 def random_tokens(parents, vocab: int, rng: np.random.Generator) -> list[int]:
-    """Uniform draft tokens, distinct among the children of each parent."""
+    """Uniform draft tokens, distinct among the children of each parent.
+
+    Raises ValueError when a parent has more children than the vocabulary has
+    tokens (no distinct assignment exists)."""
+    fanout: dict[int, int] = {}
+    for k in range(1, len(parents)):
+        fanout[parents[k]] = fanout.get(parents[k], 0) + 1
+    if fanout and max(fanout.values()) > vocab:
+        raise ValueError(f"a parent has {max(fanout.values())} children but the vocabulary "
+                         f"has only {vocab} tokens")
     used: dict[int, set[int]] = {}
     tokens = []
     for k in range(1, len(parents)):
@@ -235,6 +245,13 @@ def qwen3_4b_workload(seed: int = 2) -> AttentionWorkload:
 def qwen3_8b_workload(seed: int = 3) -> AttentionWorkload:
     return _tiered_workload("qwen3_8b_attn_64req_2048rows", seed, 64, 512, 4096,
                             [16, 32, 64, 128], None, 2048, 128)
+
+
+def tier128_workload(seed: int = 6) -> AttentionWorkload:
+    """Qwen3-8B attention shape with every request at the 128-node tier: 16
+    requests, prefixes U{512..4096}, 2048 rows (the MFMA-heaviest units)."""
+    return _tiered_workload("qwen3_8b_attn_16req_tier128", seed, 16, 512, 4096, [128], None,
+                            2048, 128)
 
 
 def long_context_workload(seed: int = 5) -> AttentionWorkload:

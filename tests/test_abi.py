@@ -1,5 +1,6 @@
 """The C-ABI library loads, exports every declared symbol, and its host-side
 planner produces a valid work list.  No GPU calls."""
+import ctypes
 import re
 from pathlib import Path
 
@@ -19,7 +20,7 @@ def _declared_functions():
 
 def test_library_loads_and_struct_sizes_match():
     lib = _lib.load()
-    assert lib.sg_abi_version() == 2
+    assert lib.sg_abi_version() == _lib.SG_ABI_VERSION == 3
 
 
 def test_every_declared_symbol_is_exported():
@@ -105,6 +106,93 @@ def test_plan_rejects_oversized_trees_and_bad_heads():
         ops.plan_attention([0, 4], [10], 30, 8, 128)
     with pytest.raises(ValueError):
         ops.plan_attention([0, 4], [10], 32, 8, 96)
+
+
+def test_head_groups_beyond_16_are_rejected_not_crashed():
+    """128 query heads per kv head used to reach a division by zero in the
+    row-split path of the planner; groups are limited to 1..16."""
+    rows = np.arange(0, 9, dtype=np.int32)
+    with pytest.raises(ValueError, match="1, 2, 4, 8 or 16"):
+        ops.plan_attention(rows, [65536] + [16] * 7, 128, 1, 128)
+    with pytest.raises(ValueError, match="1, 2, 4, 8 or 16"):
+        ops.plan_attention([0, 4], [10], 32, 1, 128)
+    ops.plan_attention(rows, [65536] + [16] * 7, 16, 1, 128)  # the largest group plans
+
+
+def _attn_args(**fields):
+    """SgTreeAttnArgs with placeholder device pointers: every call below must
+    be rejected by the host-side checks before anything touches a device."""
+    a = _lib.SgTreeAttnArgs()
+    a.num_requests, a.num_rows, a.num_q_heads, a.num_kv_heads, a.head_dim = 1, 4, 8, 2, 128
+    a.scale = 128 ** -0.5
+    for name in ("q_dev", "k_cache_dev", "v_cache_dev", "k_tree_dev", "v_tree_dev",
+                 "row_offset_dev", "prefix_start_dev", "prefix_len_dev", "parent_dev",
+                 "out_dev", "plan_dev"):
+        setattr(a, name, 0x1000)
+    a.q_row_stride, a.q_head_stride = 8 * 128, 128
+    a.cache_head_stride, a.cache_token_stride = 128 * 1024, 128
+    a.tree_row_stride, a.tree_head_stride = 2 * 128, 128
+    a.out_row_stride, a.out_head_stride = 8 * 128, 128
+    a.plan_units = 1
+    for k, v in fields.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_fwd_rejects_bad_head_counts_without_crashing():
+    lib = _lib.load()
+    for hq, hkv in ((0, 2), (0, 0), (3, 2), (256, 2), (8, -1)):
+        a = _attn_args(num_q_heads=hq, num_kv_heads=hkv)
+        assert lib.sg_tree_attn_fwd(ctypes.byref(a), None) == _lib.SG_EINVAL, (hq, hkv)
+
+
+def test_stale_plans_are_rejected_on_the_host():
+    """A plan records its wave: the planner's header keeps the request and row
+    counts and a hash of the row offsets and prefix lengths."""
+    row_offset, prefix = [0, 4, 9], [100, 37]
+    plan = ops.plan_attention(row_offset, prefix, 8, 2, 128)
+    assert plan.num_requests == 2 and plan.num_rows == 9
+    ops.check_plan(plan, row_offset, prefix)
+    with pytest.raises(ValueError, match="another wave"):
+        ops.check_plan(plan, row_offset, [100, 40])      # after a commit of 3 rows
+    with pytest.raises(ValueError, match="another wave"):
+        ops.check_plan(plan, [0, 5, 9], prefix)
+    with pytest.raises(ValueError, match="another wave"):
+        ops.check_plan_call(plan, 2, 10, 8, 2, 128)
+    with pytest.raises(ValueError, match="head configuration"):
+        ops.check_plan_call(plan, 2, 9, 16, 2, 128)
+    # The C ABI checks the host copy of the plan before enqueueing anything.
+    lib = _lib.load()
+    for fields in ({"num_rows": 10}, {"num_requests": 3}, {"num_q_heads": 16},
+                   {"plan_units": plan.units + 1}):
+        base = dict(num_requests=2, num_rows=9, plan_units=plan.units,
+                    plan_merges=plan.merges, plan_host=plan.host.ctypes.data)
+        base.update(fields)
+        a = _attn_args(**base)
+        assert lib.sg_tree_attn_fwd(ctypes.byref(a), None) == _lib.SG_EINVAL, fields
+        assert b"plan" in lib.sg_last_error()
+
+
+def test_noalloc_sampler_rejects_oversized_waves_before_any_device_call():
+    lib = _lib.load()
+    a = _lib.SgTreeSampleArgs()
+    per_request = lib.sg_tree_sample_workspace_bytes(1, 151936)
+    a.num_requests = _lib.NOALLOC_SCRATCH_BYTES // per_request + 1
+    a.num_rows = a.num_requests
+    a.vocab = 151936
+    a.logits_row_stride = 151936
+    a.uniform_stride = 2
+    for name in ("logits_dev", "row_offset_dev", "parent_dev", "token_dev", "uniforms_dev",
+                 "row_max_dev", "row_sum_dev", "accept_len_dev", "bonus_dev"):
+        setattr(a, name, 0x1000)
+    assert lib.sg_tree_sample_noalloc(ctypes.byref(a), None) == _lib.SG_EINVAL
+    assert b"static maximum" in lib.sg_last_error()
+    a.num_requests = a.num_rows = 2
+    a.workspace_dev, a.workspace_bytes = 0x1000, 1 << 20
+    assert lib.sg_tree_sample_noalloc(ctypes.byref(a), None) == _lib.SG_EINVAL
+    a.workspace_dev, a.workspace_bytes = 0, 0
+    a.logits_dtype = 7
+    assert lib.sg_tree_sample_noalloc(ctypes.byref(a), None) == _lib.SG_EINVAL
 
 
 def test_product_package_never_imports_the_oracle():

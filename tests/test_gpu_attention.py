@@ -219,3 +219,40 @@ def test_random_head_groups_prefixes_and_tree_forms(device, oracle, hq, hkv, dim
     for i in live:
         r0, r1 = int(wl.row_offset[i]), int(wl.row_offset[i + 1])
         _assert_close(got[r0:r1], refs[i])
+
+
+def test_plan_of_another_wave_is_caught_on_the_device(device, oracle):
+    """A plan built for other prefix lengths (as after a commit) reads no K/V
+    for its mismatched units: they raise the status word and write NaN; with
+    the right plan the same call is clean.  Covers plans whose prefixes are
+    shorter and longer than the call's, unsplit and split (merge) plans."""
+    split_wl = W.qwen3_4b_workload(seed=21)
+    _, split_dev, split_meta = _inputs(split_wl, device, 17)
+    wl = W.tiny_attention_workload(seed=5, num_q_heads=8, num_kv_heads=2, head_dim=128)
+    tensors, dev, meta = _inputs(wl, device, 16)
+    for case_wl, case_dev, case_meta, delta, target in (
+            (wl, dev, meta, 3, 0), (wl, dev, meta, -5, 0),
+            (split_wl, split_dev, split_meta, 3, 4096)):
+        stale = ops.plan_attention(case_wl.row_offset, case_wl.prefix_len + delta,
+                                   case_wl.num_q_heads, case_wl.num_kv_heads,
+                                   case_wl.head_dim, target).to(device)
+        assert target == 0 or stale.merges > 0
+        status = torch.zeros(1, dtype=torch.int32, device=device)
+        q, kc, vc, kt, vt = case_dev
+        out = ops.tree_attention(q, kc, vc, kt, vt, case_meta["row_offset"],
+                                 case_meta["prefix_start"], case_meta["prefix_len"],
+                                 case_meta["parent"], stale, status=status)
+        torch.cuda.synchronize()
+        assert int(status.item()) == ops._lib.SG_EINVAL, (delta, target)
+        assert torch.isnan(out.float()).all(), (delta, target)
+    q, kc, vc, kt, vt = dev
+    good = ops.plan_attention(wl.row_offset, wl.prefix_len, 8, 2, 128).to(device)
+    ops.check_plan(good, wl.row_offset, wl.prefix_len)
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    out = ops.tree_attention(q, kc, vc, kt, vt, meta["row_offset"], meta["prefix_start"],
+                             meta["prefix_len"], meta["parent"], good, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0 and torch.isfinite(out.float()).all()
+    with pytest.raises(ValueError, match="another wave"):
+        ops.tree_attention(q[:-1], kc, vc, kt[:-1], vt[:-1], meta["row_offset"],
+                           meta["prefix_start"], meta["prefix_len"], meta["parent"], good)

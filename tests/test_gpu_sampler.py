@@ -191,3 +191,39 @@ def test_random_trees_vocabularies_and_acceptance_rates(device, oracle, seed):
                         logit_std=float(rng.choice([0.5, 3.0, 6.0])),
                         extreme_uniforms=bool(seed % 3 == 0))
     _check_case(case, device, oracle)
+
+
+def test_reused_outputs_must_fit_the_call(device, oracle):
+    """Caller-supplied outputs are checked against n, R and max_depth, and the
+    status word left by an earlier broken call is cleared by the next call."""
+    case = tree_problem(51, num_requests=4, nodes=[9, 5, 7, 3], vocab=1000)
+    t = {k: torch.from_numpy(case[k]).to(device)
+         for k in ("logits", "row_offset", "parent", "token", "uniforms")}
+    res = ops.tree_sample(t["logits"], t["row_offset"], t["parent"], t["token"],
+                          t["uniforms"], case["max_depth"])
+    small = tree_problem(52, num_requests=2, nodes=[3, 2], vocab=1000)
+    ts = {k: torch.from_numpy(small[k]).to(device)
+          for k in ("logits", "row_offset", "parent", "token", "uniforms")}
+    with pytest.raises(ValueError, match="out\\."):
+        ops.tree_sample(ts["logits"], ts["row_offset"], ts["parent"], ts["token"],
+                        ts["uniforms"], small["max_depth"], out=res)
+    # A request whose rows run past num_rows is a broken walk (status EINVAL,
+    # accept length -1); the next call on the same outputs starts clean.
+    bad_offset = t["row_offset"].clone()
+    bad_offset[-1] += 3
+    parent_pad = torch.cat([t["parent"], torch.zeros(3, dtype=torch.int32, device=device)])
+    token_pad = torch.cat([t["token"], torch.zeros(3, dtype=torch.int32, device=device)])
+    res = ops.tree_sample(t["logits"], bad_offset, parent_pad, token_pad, t["uniforms"],
+                          case["max_depth"], out=res)
+    torch.cuda.synchronize()
+    assert int(res.status.item()) == ops._lib.SG_EINVAL
+    assert int(res.accept_len[-1].item()) == -1
+    res = ops.tree_sample(t["logits"], t["row_offset"], t["parent"], t["token"],
+                          t["uniforms"], case["max_depth"], out=res)
+    torch.cuda.synchronize()
+    assert int(res.status.item()) == 0
+    nodes, length, bonus, _, _ = oracle.tree_sample(
+        case["logits"], case["row_offset"], case["parent"], case["token"],
+        case["uniforms"], case["max_depth"])
+    np.testing.assert_array_equal(res.accept_len.cpu().numpy(), length)
+    np.testing.assert_array_equal(res.bonus.cpu().numpy(), bonus)
