@@ -61,6 +61,9 @@ def parse_args():
                    help="for hardware-counter runs: --steps attention calls on the rotating "
                         "input sets, then one 1 GiB device copy whose counter readings "
                         "calibrate FETCH_SIZE / WRITE_SIZE; prints nothing")
+    p.add_argument("--counters-workload", default="qwen3_8b",
+                   choices=["qwen3_8b", "qwen3_4b", "tier128", "long_context"],
+                   help="the attention wave of a --counters-only run")
     return p.parse_args()
 
 
@@ -398,11 +401,15 @@ def read_traffic():
     return data.get("hbm_bytes_per_launch"), source
 
 
-def counters_only(torch, np, W, ops, device, steps, warmup):
+def counters_only(torch, np, W, ops, device, steps, warmup, workload="qwen3_8b"):
     """Attention calls plus a copy of known size, for rocprofv3 --pmc runs."""
-    wl, plan, meta, sets = build_attention_sets(torch, np, W, ops, device, 4)
+    make = {"qwen3_8b": W.qwen3_8b_workload, "qwen3_4b": W.qwen3_4b_workload,
+            "tier128": W.tier128_workload, "long_context": W.long_context_workload}[workload]
+    sets_n = 1 if workload == "long_context" else N_SETS
+    wl, plan, meta, sets = build_attention_sets(torch, np, W, ops, device, 4, wl=make(),
+                                                sets=sets_n)
     for k in range(warmup + steps):
-        attention_call(ops, wl, plan, meta, sets[k % N_SETS])
+        attention_call(ops, wl, plan, meta, sets[k % sets_n])
     torch.cuda.synchronize()
     src = torch.empty(1 << 30, dtype=torch.uint8, device=device).fill_(1)
     dst = torch.empty_like(src)
@@ -428,7 +435,7 @@ def main():
     torch.cuda.init()
     steps, warmup = args.steps, args.warmup
     if args.counters_only:
-        counters_only(torch, np, W, ops, device, steps, warmup)
+        counters_only(torch, np, W, ops, device, steps, warmup, args.counters_workload)
         return
     wl, plan, meta, sets = build_attention_sets(torch, np, W, ops, device,
                                                 4 * (steps + warmup) + 16)

@@ -34,6 +34,7 @@
 #include <climits>
 #include <cstring>
 #include <numeric>
+#include <queue>
 #include <type_traits>
 #include <vector>
 
@@ -975,11 +976,11 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
   const int rows_per_tile = kQPerUnit / G;
   SG_REQUIRE(num_requests == 0 || row_offset_host[0] == 0, "row_offset[0] must be 0");
 
-  // Units of one (request, kv head, row tile) are split over its prefix only
-  // when the wave has too few units to give every CU work: each split costs a
-  // partial write and a merge pass.  target_units_hint overrides the target.
+  // Units of one (request, kv head, row tile) are split over their prefix when
+  // the wave has too few units to give every CU slot work, or when one would
+  // dominate the end of the launch: each split costs a partial write and a
+  // merge pass.  target_units_hint overrides the slot count.
   int64_t base_units = 0;
-  int64_t work = 0;
   for (int i = 0; i < num_requests; ++i) {
     const int rows = row_offset_host[i + 1] - row_offset_host[i];
     SG_REQUIRE(rows >= 0 && rows <= kMaxTreeRows,
@@ -987,24 +988,51 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
     SG_REQUIRE(prefix_len_host[i] >= 0, "prefix lengths must be non-negative");
     const int tiles = (rows + rows_per_tile - 1) / rows_per_tile;
     base_units += static_cast<int64_t>(num_kv_heads) * tiles;
-    work += static_cast<int64_t>(num_kv_heads) * tiles *
-            ((prefix_len_host[i] + kTileKeys - 1) / kTileKeys + 1);
   }
   const int64_t target = target_units_hint > 0 ? target_units_hint : kDefaultCUs * kListsPerCU;
-  int64_t chunk = INT32_MAX;
-  if (base_units > 0 && base_units < target) {
-    const int64_t per_unit = std::max<int64_t>(4, (work + target - 1) / target);
-    chunk = per_unit * kTileKeys;
+  auto unit_cost = [&](int row_count, int64_t tiles) -> int64_t {
+    const int nq = (row_count * G + 31) / 32;
+    return nq <= 2 ? 550 + 57 * tiles : 840 + 88 * tiles;
+  };
+
+  // Small waves (fewer (request, kv head, row tile) units than the launch has
+  // slots) are latency-bound: every unit of request i is cut into
+  // small_splits[i] key ranges, chosen greedily -- the request whose pieces
+  // cost most gets one more piece -- while the wave stays within `target`
+  // units (one dispatch round, no unit waits for a slot) and pieces keep at
+  // least four tiles of prefix.  No row splits: they would add units.
+  const bool small_wave = base_units > 0 && base_units < target;
+  std::vector<int> small_splits(num_requests, 1);
+  if (small_wave) {
+    auto piece_cost = [&](int i, int pieces) -> int64_t {
+      const int rows = row_offset_host[i + 1] - row_offset_host[i];
+      const int64_t prefix_tiles = (prefix_len_host[i] + kTileKeys - 1) / kTileKeys;
+      const int64_t tree_tiles = (rows + kTileKeys - 1) / kTileKeys;
+      return unit_cost(std::min(rows, rows_per_tile),
+                       (prefix_tiles + pieces - 1) / pieces + tree_tiles);
+    };
+    int64_t total = base_units;
+    std::priority_queue<std::pair<int64_t, int>> heap;  // (piece cost, request)
+    for (int i = 0; i < num_requests; ++i)
+      if (row_offset_host[i + 1] > row_offset_host[i]) heap.push({piece_cost(i, 1), i});
+    while (!heap.empty()) {
+      const int i = heap.top().second;
+      heap.pop();
+      const int rows = row_offset_host[i + 1] - row_offset_host[i];
+      const int next = small_splits[i] + 1;
+      const int64_t add =
+          static_cast<int64_t>(num_kv_heads) * ((rows + rows_per_tile - 1) / rows_per_tile);
+      if (total + add > target || prefix_len_host[i] / next < 4 * kTileKeys) continue;
+      small_splits[i] = next;
+      total += add;
+      heap.push({piece_cost(i, next), i});
+    }
   }
 
   // Balance: a unit costing more than kSplitAbovePercent % of a CU slot's
   // mean share is split over its prefix into pieces below that bound, so that
   // no unit dominates the end of the launch (each piece costs a prologue, a
   // partial write and a merge, so the bound is high).
-  auto unit_cost = [&](int row_count, int64_t tiles) -> int64_t {
-    const int nq = (row_count * G + 31) / 32;
-    return nq <= 2 ? 550 + 57 * tiles : 840 + 88 * tiles;
-  };
   std::vector<int> balance_splits(num_requests, 1);
   std::vector<char> split_rows(num_requests, 0);
   {
@@ -1041,13 +1069,12 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
     // 64 query vectors (half a row tile), which read the same K/V on one XCD
     // (L2 serves the second read) and need no merge; only a unit of at most
     // 64 query vectors is split over its prefix.
-    const bool row_split = split_rows[i] != 0;
+    const bool row_split = !small_wave && split_rows[i] != 0;
     const int rpt = row_split ? rows_per_tile / 2 : rows_per_tile;
     // Pieces keep at least four full tiles of prefix.
-    const int splits = std::max(1, std::min(std::max(row_split ? 1 : balance_splits[i],
-                                                     static_cast<int>(std::max<int64_t>(
-                                                         1, (L + chunk / 2) / chunk))),
-                                            L / (4 * kTileKeys)));
+    const int splits =
+        small_wave ? small_splits[i]
+                   : std::max(1, std::min(row_split ? 1 : balance_splits[i], L / (4 * kTileKeys)));
     const int tiles = (rows + rpt - 1) / rpt;
     for (int g = 0; g < num_kv_heads; ++g) {
       for (int tile = 0; tile < tiles; ++tile) {
