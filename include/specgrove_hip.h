@@ -168,6 +168,49 @@ typedef struct SgKvCommitArgs {
 int sg_kv_commit(const SgKvCommitArgs* args, sg_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * (B') Non-persistent split: rebuild every request's cache from one packed
+ * wave, all layers in one launch.
+ *
+ * Replaces _split_compacted_sequence_caches (CTBD:409-450), the path taken
+ * without the persistent arena: request i's new cache is its old prefix
+ * (L_i tokens at c_i of the packed prefix) followed by its kept tree rows,
+ *   out[l][g, o_i + t]       = prefix[l][g, c_i + t]                t < L_i
+ *   out[l][g, o_i + L_i + t] = tree[l][q_i + keep_i[t], g]          t < keep_len_i
+ * with q_i = row_offset[i].  A kept row outside [0, row_offset[i+1] - q_i), or
+ * L_i + keep_len_i above max_tokens, is not copied and sets *status_dev to
+ * SG_EINVAL.
+ * ---------------------------------------------------------------------- */
+typedef struct SgKvSplitArgs {
+  int32_t num_layers;
+  int32_t num_requests;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t max_tokens;              /* >= max_i (L_i + keep_len_i) */
+  int32_t keep_stride;
+  /* packed prefix per layer: element (head g, token t) at base + g*head_stride + t*token_stride */
+  const void* const* k_prefix_layers_dev;
+  const void* const* v_prefix_layers_dev;
+  int64_t prefix_head_stride, prefix_token_stride;
+  /* this wave's tree-row K/V per layer [R, Hkv, D] */
+  const void* const* k_tree_layers_dev;
+  const void* const* v_tree_layers_dev;
+  int64_t tree_row_stride, tree_head_stride;
+  /* new caches per layer, same element addressing as the prefix */
+  void* const* k_out_layers_dev;
+  void* const* v_out_layers_dev;
+  int64_t out_head_stride, out_token_stride;
+  const int64_t* cache_offset_dev; /* [n] c_i */
+  const int32_t* old_length_dev;   /* [n] L_i */
+  const int32_t* row_offset_dev;   /* [n+1] */
+  const int32_t* keep_rows_dev;    /* [n, keep_stride] local rows, ascending path order */
+  const int32_t* keep_len_dev;     /* [n] */
+  const int64_t* out_offset_dev;   /* [n] o_i, first token of request i's new cache */
+  int32_t* status_dev;             /* optional [1]; SG_EINVAL, never cleared */
+} SgKvSplitArgs;
+
+int sg_kv_split(const SgKvSplitArgs* args, sg_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * (C) Temperature-1 tree rejection sampling over a packed wave.
  *
  * Replaces the fp32 softmax + ancestral verification of the formal path
@@ -239,7 +282,8 @@ int sg_row_stats(const void* logits_dev, int32_t logits_dtype, int64_t row_strid
                  sg_stream_t stream);
 
 /* sizeof() of the argument structs as compiled into the library, for binding
- * checks: which = 0 SgTreeAttnArgs, 1 SgKvCommitArgs, 2 SgTreeSampleArgs.
+ * checks: which = 0 SgTreeAttnArgs, 1 SgKvCommitArgs, 2 SgTreeSampleArgs,
+ * 3 SgKvSplitArgs.
  * Returns -1 for an unknown index.  No reference counterpart. */
 int64_t sg_abi_struct_size(int32_t which);
 

@@ -393,6 +393,27 @@ def kv_commit(arena_k: np.ndarray, arena_v: np.ndarray, lengths: np.ndarray,
     return lengths
 
 
+def kv_split(prefix_k: np.ndarray, prefix_v: np.ndarray, tree_k: np.ndarray,
+             tree_v: np.ndarray, cache_offsets: Sequence[int], old_lengths: Sequence[int],
+             row_offset: Sequence[int], keep_rows: Sequence[Sequence[int]]):
+    """Non-persistent split (CTBD:409-450): request i's new cache is the packed
+    prefix rows [c_i, c_i + L_i) followed by its kept tree rows q_i + keep_i[t].
+
+    prefix_k/v [layers, Hkv, P, D]; tree_k/v [layers, R, Hkv, D].  Returns a
+    list of (keys, values) [layers, Hkv, L_i + |keep_i|, D] per request.
+    """
+    out = []
+    for i, keep in enumerate(keep_rows):
+        c, length, q = int(cache_offsets[i]), int(old_lengths[i]), int(row_offset[i])
+        rows = [q + int(r) for r in keep]
+        keys = np.concatenate([prefix_k[:, :, c:c + length],
+                               tree_k[:, rows].transpose(0, 2, 1, 3)], axis=2)
+        values = np.concatenate([prefix_v[:, :, c:c + length],
+                                 tree_v[:, rows].transpose(0, 2, 1, 3)], axis=2)
+        out.append((keys, values))
+    return out
+
+
 def cpu_model() -> str:
     """The host CPU's model name (from /proc/cpuinfo when available)."""
     try:

@@ -61,6 +61,23 @@ class SgKvCommitArgs(ctypes.Structure):
     ]
 
 
+class SgKvSplitArgs(ctypes.Structure):
+    _fields_ = [
+        ("num_layers", c_i32), ("num_requests", c_i32), ("num_kv_heads", c_i32),
+        ("head_dim", c_i32), ("max_tokens", c_i32), ("keep_stride", c_i32),
+        ("k_prefix_layers_dev", c_void_p), ("v_prefix_layers_dev", c_void_p),
+        ("prefix_head_stride", c_i64), ("prefix_token_stride", c_i64),
+        ("k_tree_layers_dev", c_void_p), ("v_tree_layers_dev", c_void_p),
+        ("tree_row_stride", c_i64), ("tree_head_stride", c_i64),
+        ("k_out_layers_dev", c_void_p), ("v_out_layers_dev", c_void_p),
+        ("out_head_stride", c_i64), ("out_token_stride", c_i64),
+        ("cache_offset_dev", c_void_p), ("old_length_dev", c_void_p),
+        ("row_offset_dev", c_void_p), ("keep_rows_dev", c_void_p),
+        ("keep_len_dev", c_void_p), ("out_offset_dev", c_void_p),
+        ("status_dev", c_void_p),
+    ]
+
+
 class SgTreeSampleArgs(ctypes.Structure):
     _fields_ = [
         ("num_requests", c_i32), ("num_rows", c_i32), ("vocab", c_i32),
@@ -81,7 +98,7 @@ EXPORTED_SYMBOLS = (
     "sg_abi_version", "sg_last_error", "sg_abi_struct_size",
     "sg_tree_attn_plan", "sg_tree_attn_fwd", "sg_kv_commit",
     "sg_tree_sample", "sg_tree_sample_workspace_bytes", "sg_row_stats", "sg_exp_probe",
-    "sg_tree_sample_noalloc", "sg_tree_attn_plan_check",
+    "sg_tree_sample_noalloc", "sg_tree_attn_plan_check", "sg_kv_split",
 )
 
 # Static scratch of sg_tree_sample_noalloc (SG_TREE_SAMPLE_NOALLOC_SCRATCH_BYTES).
@@ -122,6 +139,8 @@ def load() -> ctypes.CDLL:
     lib.sg_tree_attn_fwd.argtypes = [ctypes.POINTER(SgTreeAttnArgs), c_void_p]
     lib.sg_kv_commit.restype = c_i32
     lib.sg_kv_commit.argtypes = [ctypes.POINTER(SgKvCommitArgs), c_void_p]
+    lib.sg_kv_split.restype = c_i32
+    lib.sg_kv_split.argtypes = [ctypes.POINTER(SgKvSplitArgs), c_void_p]
     lib.sg_tree_sample.restype = c_i32
     lib.sg_tree_sample.argtypes = [ctypes.POINTER(SgTreeSampleArgs), c_void_p]
     lib.sg_tree_sample_noalloc.restype = c_i32
@@ -138,7 +157,7 @@ def load() -> ctypes.CDLL:
         raise RuntimeError(f"ABI mismatch: the library is version {version}, the binding "
                            f"version {SG_ABI_VERSION}; rebuild with `python -m "
                            f"specgrove_amd.build`")
-    expected = {0: SgTreeAttnArgs, 1: SgKvCommitArgs, 2: SgTreeSampleArgs}
+    expected = {0: SgTreeAttnArgs, 1: SgKvCommitArgs, 2: SgTreeSampleArgs, 3: SgKvSplitArgs}
     for which, struct in expected.items():
         size = lib.sg_abi_struct_size(which)
         if size != ctypes.sizeof(struct):

@@ -39,7 +39,9 @@ IMPLEMENTATION = "specgrove_hip"
 @dataclass
 class PackedTreeMask:
     """Compact replacement of the packed dense mask."""
-    pool: object                    # PersistentRequestCachePool (arena per layer)
+    pool: object                    # the prefixes: a PersistentRequestCachePool (arena per
+                                    # layer) or a PackedPrefix (non-persistent wave); both
+                                    # expose key_storage[l] / value_storage[l] [Hkv, T, D]
     row_offset: torch.Tensor        # [n+1] i32, device
     parent: torch.Tensor            # [R] i32, request-local parents, -1 for roots
     prefix_start: torch.Tensor      # [n] i64, slot * capacity
@@ -64,10 +66,13 @@ class PackedTreeMask:
 
 
 def build_tree_mask(pool, caches: Sequence, parents_list: Sequence[Sequence[int]],
-                    device) -> PackedTreeMask:
+                    device, prefix_start: Sequence[int] | None = None,
+                    prefix_len: Sequence[int] | None = None) -> PackedTreeMask:
     """Compact mask of one wave: request i uses arena slot ``caches[i].slot``
-    with its current length as prefix and the tree ``parents_list[i]`` (local
-    parent indices, root -1, parents before children)."""
+    with its current length as prefix (or, for a non-persistent wave, the
+    given ``prefix_start`` / ``prefix_len`` in ``pool``, a PackedPrefix) and
+    the tree ``parents_list[i]`` (local parent indices, root -1, parents
+    before children)."""
     rows = [len(p) for p in parents_list]
     row_offset = np.zeros(len(rows) + 1, np.int32)
     np.cumsum(rows, out=row_offset[1:])
@@ -76,15 +81,28 @@ def build_tree_mask(pool, caches: Sequence, parents_list: Sequence[Sequence[int]
     for p in parents_list:
         if len(p) == 0 or p[0] != -1 or any(not 0 <= q < k for k, q in enumerate(p[1:], 1)):
             raise ValueError("Tree parents must precede their children")
-    prefix_len = np.asarray([pool.lengths[c.slot] for c in caches], np.int32)
-    prefix_start = np.asarray([c.slot * pool.capacity for c in caches], np.int64)
+    if prefix_start is None:
+        prefix_len = np.asarray([pool.lengths[c.slot] for c in caches], np.int32)
+        prefix_start = np.asarray([c.slot * pool.capacity for c in caches], np.int64)
+    else:
+        prefix_len = np.asarray(prefix_len, np.int32)
+        prefix_start = np.asarray(prefix_start, np.int64)
     dev = torch.device(device)
+    # One host-to-device copy for the whole wave: prefix starts (int64), then
+    # row offsets, prefix lengths and parents as int32 pairs.
+    n = len(rows)
+    words32 = np.concatenate([row_offset, prefix_len, parent]).astype(np.int32)
+    if words32.size % 2:
+        words32 = np.concatenate([words32, np.zeros(1, np.int32)])
+    host = np.concatenate([prefix_start.astype(np.int64), words32.view(np.int64)])
+    meta = torch.from_numpy(host).to(dev)
+    meta32 = meta[n:].view(torch.int32)
     return PackedTreeMask(
         pool=pool,
-        row_offset=torch.from_numpy(row_offset).to(dev),
-        parent=torch.from_numpy(parent).to(dev),
-        prefix_start=torch.from_numpy(prefix_start).to(dev),
-        prefix_len=torch.from_numpy(prefix_len).to(dev),
+        row_offset=meta32[:n + 1],
+        parent=meta32[2 * n + 1:2 * n + 1 + parent.size],
+        prefix_start=meta[:n],
+        prefix_len=meta32[n + 1:2 * n + 1],
         row_offset_host=row_offset,
         prefix_len_host=prefix_len,
     )
@@ -97,8 +115,10 @@ def pack_block_inputs(states, blocks, cache_lengths: Sequence[int],
     Same ``ids`` [1, R], ``positions`` [1, R] and ``query_offsets``; the
     third result is ``{"full_attention": PackedTreeMask}`` instead of the
     dense ``[1, 1, R, P + R]`` mask.  ``states[i].target_cache`` must be a
-    view of one persistent pool; ``cache_offsets``, ``packed_cache_length``
-    and ``dtype`` are accepted for signature compatibility.
+    view of one persistent pool, or the request caches just packed by
+    ``pack_cache_sequence`` (non-persistent wave, prefixes at
+    ``cache_offsets``); ``packed_cache_length`` and ``dtype`` are accepted for
+    signature compatibility.
     """
     block_rows = tuple(len(block.nodes) for block in blocks)
     query_offsets = []
@@ -115,12 +135,26 @@ def pack_block_inputs(states, blocks, cache_lengths: Sequence[int],
         ids[q0:q0 + rows] = [root] + list(block.tokens)
         positions[q0:q0 + rows] = np.asarray(block.depths, np.int64) + state.round_prefix_len
     caches = [state.target_cache for state in states]
-    pool = caches[0].pool
-    if any(c.pool is not pool for c in caches):
-        raise ValueError("Packed tree verification needs caches of one persistent pool")
-    if any(pool.lengths[c.slot] != int(L) for c, L in zip(caches, cache_lengths)):
-        raise ValueError("Cache lengths disagree with the persistent pool")
-    mask = build_tree_mask(pool, caches, [list(block.parents) for block in blocks], device)
+    parents_list = [list(block.parents) for block in blocks]
+    if hasattr(caches[0], "pool") and hasattr(caches[0], "slot"):
+        pool = caches[0].pool
+        if any(getattr(c, "pool", None) is not pool for c in caches):
+            raise ValueError("Packed tree verification needs caches of one persistent pool")
+        if any(pool.lengths[c.slot] != int(L) for c, L in zip(caches, cache_lengths)):
+            raise ValueError("Cache lengths disagree with the persistent pool")
+        mask = build_tree_mask(pool, caches, parents_list, device)
+    else:
+        # Non-persistent wave: the prefixes were packed by pack_cache_sequence.
+        from .cache import packed_wave_of
+        wave = packed_wave_of(caches[0])
+        if wave is None or any(packed_wave_of(c) is not wave for c in caches) \
+                or tuple(wave.caches) != tuple(caches):
+            raise ValueError("Request caches were not packed together by pack_cache_sequence")
+        if (tuple(int(v) for v in cache_lengths) != wave.prefix_lengths
+                or tuple(int(v) for v in cache_offsets) != wave.prefix_starts):
+            raise ValueError("Cache lengths disagree with the packed wave")
+        mask = build_tree_mask(wave.prefix_source, caches, parents_list, device,
+                               prefix_start=wave.prefix_starts, prefix_len=wave.prefix_lengths)
     dev = torch.device(device)
     return (torch.from_numpy(ids).to(dev).unsqueeze(0),
             torch.from_numpy(positions).to(dev).unsqueeze(0),

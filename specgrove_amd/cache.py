@@ -22,6 +22,7 @@ exhausted") before anything is written.
 """
 from __future__ import annotations
 
+import weakref
 from typing import Sequence
 
 import numpy as np
@@ -114,18 +115,16 @@ class PersistentRequestCachePool:
             self.value_storage.append(values)
         self.device = self.key_storage[0].device
         self.caches = tuple(PersistentRequestCache(self, slot) for slot in range(len(caches)))
-        self._lengths_dev = None
         self._k_ptrs = None
         self._v_ptrs = None
 
     # -- device mirrors ---------------------------------------------------
-    def _device_state(self):
-        if self._lengths_dev is None:
-            dev = self.device
-            self._lengths_dev = torch.tensor(self.lengths, dtype=torch.int32, device=dev)
-            self._k_ptrs = ops.pointer_array(self.key_storage, dev)
-            self._v_ptrs = ops.pointer_array(self.value_storage, dev)
-        return self._lengths_dev, self._k_ptrs, self._v_ptrs
+    def _device_pointers(self):
+        """Per-layer arena bases on the device, built once per pool."""
+        if self._k_ptrs is None:
+            self._k_ptrs = ops.pointer_array(self.key_storage, self.device)
+            self._v_ptrs = ops.pointer_array(self.value_storage, self.device)
+        return self._k_ptrs, self._v_ptrs
 
     def slot_starts(self, caches: Sequence[PersistentRequestCache]) -> list[int]:
         return [cache.slot * self.capacity for cache in caches]
@@ -174,27 +173,37 @@ class PersistentRequestCachePool:
         for i, rows in enumerate(keep_query_rows):
             keep[i, :len(rows)] = [int(r) for r in rows]
         slots = [cache.slot for cache in caches]
-        lengths_dev, k_ptrs, v_ptrs = self._device_state()
+        k_ptrs, v_ptrs = self._device_pointers()
         dev = self.device
-        # Commit runs over the caller's subset of slots: gather their lengths,
-        # advance them in the kernel, and scatter them back.
-        slot_index = torch.tensor(slots, dtype=torch.long, device=dev)
-        sub_lengths = lengths_dev.index_select(0, slot_index).contiguous()
+        layers = len(packed.layers)
+        # One host-to-device copy: the wave's tree-row pointers per layer, the
+        # requests' slot starts (int64), then row offsets, kept rows, keep
+        # lengths and the current lengths (int32 pairs).  The host lengths are
+        # authoritative; the kernel advances this wave's copy of them.
+        tree_ptrs = [layer.tree_keys.data_ptr() for layer in packed.layers] + \
+                    [layer.tree_values.data_ptr() for layer in packed.layers]
+        words32 = np.concatenate([
+            row_offset.astype(np.int32), keep.reshape(-1),
+            np.asarray([len(r) for r in keep_query_rows], np.int32),
+            np.asarray([self.lengths[s] for s in slots], np.int32)])
+        if words32.size % 2:
+            words32 = np.concatenate([words32, np.zeros(1, np.int32)])
+        host = np.concatenate([np.asarray(tree_ptrs, np.int64),
+                               np.asarray([s * self.capacity for s in slots], np.int64),
+                               words32.view(np.int64)])
+        meta = torch.from_numpy(host).to(dev)
+        meta32 = meta[2 * layers + n:].view(torch.int32)
+        w = keep.size
         k0 = self.key_storage[0]
         kt = packed.layers[0].tree_keys
         ops.kv_commit(
-            k_ptrs, v_ptrs, packed.key_pointers(), packed.value_pointers(),
+            k_ptrs, v_ptrs, meta[:layers], meta[layers:2 * layers],
             num_kv_heads=k0.shape[0], head_dim=k0.shape[2],
             cache_head_stride=k0.stride(0), cache_token_stride=k0.stride(1),
             tree_row_stride=kt.stride(0), tree_head_stride=kt.stride(1),
-            row_offset=torch.from_numpy(row_offset.astype(np.int32)).to(dev),
-            keep_rows=torch.from_numpy(keep).to(dev),
-            keep_len=torch.tensor([len(r) for r in keep_query_rows], dtype=torch.int32,
-                                  device=dev),
-            prefix_start=torch.tensor([s * self.capacity for s in slots], dtype=torch.int64,
-                                      device=dev),
-            lengths=sub_lengths, capacity=self.capacity)
-        lengths_dev.index_copy_(0, slot_index, sub_lengths)
+            row_offset=meta32[:n + 1], keep_rows=meta32[n + 1:n + 1 + w].view(n, keep_stride),
+            keep_len=meta32[n + 1 + w:2 * n + 1 + w], prefix_start=meta[2 * layers:2 * layers + n],
+            lengths=meta32[2 * n + 1 + w:3 * n + 1 + w], capacity=self.capacity)
         for slot, increment in increments:
             self.lengths[slot] += increment
 
@@ -215,22 +224,50 @@ class _TreeLayer:
         return self.values[0].transpose(0, 1)
 
 
+class PackedPrefix:
+    """The chosen requests' prefixes concatenated along the sequence, one
+    ``[Hkv, P, D]`` buffer per layer: the packed cache of the reference's
+    non-persistent wave (``_pack_cache_sequence``, :313-361), with the same
+    ``key_storage`` / ``value_storage`` interface as the persistent arena."""
+
+    def __init__(self, key_storage: list[torch.Tensor], value_storage: list[torch.Tensor]):
+        self.key_storage = key_storage
+        self.value_storage = value_storage
+        self.device = key_storage[0].device
+
+
 class TreeVerifyCache:
     """Cache object of one packed verification wave (replaces the packed
     ``DynamicCache`` built by ``_pack_cache_sequence``).
 
     ``update`` records the wave's new K/V rows of a layer and returns them
-    unchanged; the attention function reads the requests' prefixes from the
-    pool's arena.  ``prefix_total`` is the reference's packed prefix length
-    (sum of the chosen requests' cached lengths), kept for the commit call.
+    unchanged; the attention function reads the requests' prefixes where they
+    lie: in the persistent pool's arena (``pool`` set; request i's prefix
+    starts at its slot) or in a ``PackedPrefix`` (non-persistent waves;
+    request i's prefix starts at its packed offset).  ``prefix_total`` is the
+    reference's packed prefix length (sum of the chosen requests' cached
+    lengths), kept for the commit and split calls.
     """
 
-    def __init__(self, pool: PersistentRequestCachePool,
-                 caches: Sequence[PersistentRequestCache]):
+    def __init__(self, pool: PersistentRequestCachePool | None,
+                 caches: Sequence, prefix: "PackedPrefix | None" = None,
+                 prefix_lengths: Sequence[int] | None = None):
         self.pool = pool
         self.caches = tuple(caches)
-        self.prefix_lengths = tuple(pool.lengths[c.slot] for c in self.caches)
+        if pool is not None:
+            self.prefix_source = pool
+            self.prefix_lengths = tuple(pool.lengths[c.slot] for c in self.caches)
+            self.prefix_starts = tuple(c.slot * pool.capacity for c in self.caches)
+        else:
+            self.prefix_source = prefix
+            self.prefix_lengths = tuple(int(v) for v in prefix_lengths)
+            starts, total = [], 0
+            for length in self.prefix_lengths:
+                starts.append(total)
+                total += length
+            self.prefix_starts = tuple(starts)
         self.prefix_total = int(sum(self.prefix_lengths))
+        self.device = self.prefix_source.device
         self.layers: list[_TreeLayer] = []
 
     @property
@@ -257,27 +294,163 @@ class TreeVerifyCache:
         return self.prefix_total
 
     def key_pointers(self) -> torch.Tensor:
-        return ops.pointer_array([layer.tree_keys for layer in self.layers], self.pool.device)
+        return ops.pointer_array([layer.tree_keys for layer in self.layers], self.device)
 
     def value_pointers(self) -> torch.Tensor:
-        return ops.pointer_array([layer.tree_values for layer in self.layers], self.pool.device)
+        return ops.pointer_array([layer.tree_values for layer in self.layers], self.device)
 
 
-def pack_cache_sequence(caches: Sequence[PersistentRequestCache], cache_factory=None,
-                        device=None):
-    """Drop-in for ``_pack_cache_sequence`` (reference :313-361) on arena
-    caches: returns ``(TreeVerifyCache, lengths, offsets, total)`` without
-    copying any prefix.  ``cache_factory`` is accepted for signature
-    compatibility and unused."""
+# The non-persistent packed wave of a request cache, for pack_block_inputs,
+# which the reference calls right after _pack_cache_sequence with the same
+# request caches but without the packed cache (CTBD:1772-1787).
+_WAVE_ATTR = "_specgrove_packed_wave"
+
+
+def packed_wave_of(cache) -> "TreeVerifyCache | None":
+    ref = getattr(cache, _WAVE_ATTR, None)
+    return ref() if ref is not None else None
+
+
+def pack_cache_sequence(caches: Sequence, cache_factory=None, device=None):
+    """Drop-in for ``_pack_cache_sequence`` (reference :313-361).
+
+    Arena caches of one persistent pool: returns ``(TreeVerifyCache, lengths,
+    offsets, total)`` without copying any prefix.  Other request caches
+    (``layers[l].keys/values`` [1, Hkv, L, D], e.g. DynamicCache; the
+    non-persistent path): their prefixes are concatenated into one
+    ``PackedPrefix`` per layer -- the reference's copy -- and the request
+    caches remember the wave for ``pack_block_inputs``.  ``cache_factory`` is
+    accepted for signature compatibility and unused.
+    """
     if not caches:
         raise ValueError("At least one cache is required")
-    pool = caches[0].pool
-    if any(not isinstance(c, PersistentRequestCache) or c.pool is not pool for c in caches):
-        raise ValueError("Packed tree verification needs caches of one persistent pool")
-    packed = TreeVerifyCache(pool, caches)
-    offsets = []
-    total = 0
+    if isinstance(caches[0], PersistentRequestCache):
+        pool = caches[0].pool
+        if any(not isinstance(c, PersistentRequestCache) or c.pool is not pool for c in caches):
+            raise ValueError("Packed tree verification needs caches of one persistent pool")
+        packed = TreeVerifyCache(pool, caches)
+    else:
+        lengths = [_cache_length(c) for c in caches]
+        layer_count = len(caches[0].layers)
+        if any(len(c.layers) != layer_count for c in caches):
+            raise ValueError("Target caches have different layer counts")
+        keys, values = [], []
+        for layer_index in range(layer_count):
+            k = [c.layers[layer_index].keys for c in caches]
+            v = [c.layers[layer_index].values for c in caches]
+            if any(t.shape[0] != 1 for t in k):
+                raise ValueError("Expected one request per source cache")
+            dev = k[0].device if device is None else torch.device(device)
+            keys.append(torch.cat([t[0] for t in k], dim=1).to(dev).contiguous())
+            values.append(torch.cat([t[0] for t in v], dim=1).to(dev).contiguous())
+        packed = TreeVerifyCache(None, caches, PackedPrefix(keys, values), lengths)
+        for c in caches:
+            setattr(c, _WAVE_ATTR, weakref.ref(packed))
+    offsets, total = [], 0
     for length in packed.prefix_lengths:
         offsets.append(total)
         total += length
     return packed, packed.prefix_lengths, tuple(offsets), total
+
+
+class RequestCache:
+    """Minimal per-request cache (``layers[l].keys/values`` [1, Hkv, L, D],
+    ``update``, ``get_seq_length``), the default ``cache_factory`` of
+    ``split_compacted_sequence_caches``."""
+
+    def __init__(self):
+        self.layers: list[_TreeLayer] = []
+
+    def update(self, keys: torch.Tensor, values: torch.Tensor, layer_idx: int,
+               cache_kwargs=None):
+        if layer_idx == len(self.layers):
+            self.layers.append(_TreeLayer(keys, values))
+        elif layer_idx < len(self.layers):
+            layer = self.layers[layer_idx]
+            layer.keys = torch.cat((layer.keys, keys), dim=-2)
+            layer.values = torch.cat((layer.values, values), dim=-2)
+        else:
+            raise ValueError("Layers must be updated in order")
+        return self.layers[layer_idx].keys, self.layers[layer_idx].values
+
+    def get_seq_length(self, layer_idx: int = 0) -> int:
+        return int(self.layers[layer_idx].keys.shape[-2]) if self.layers else 0
+
+
+def split_compacted_sequence_caches(packed: TreeVerifyCache, cache_factory,
+                                    cache_offsets: Sequence[int], old_lengths: Sequence[int],
+                                    packed_old_length: int, query_offsets: Sequence[int],
+                                    keep_query_rows: Sequence[Sequence[int]], device):
+    """Drop-in for ``_split_compacted_sequence_caches`` (reference :409-450):
+    every request's new cache = its old prefix + its kept query rows, for all
+    layers in one ``sg_kv_split`` call.
+
+    The new caches are views of one ``[Hkv, sum(L_i + |keep_i|), D]`` buffer
+    per layer (as the reference's slices of its one gather per layer), handed
+    to ``cache_factory()`` caches through ``update`` (``RequestCache`` when
+    ``cache_factory`` is None).  The source row of request i's kept row k is
+    ``query_offsets[i] + k`` of the wave's new rows (the reference's
+    ``packed_old_length + query_offsets[i] + k``).
+    """
+    count = len(cache_offsets)
+    if not (count == len(old_lengths) == len(query_offsets) == len(keep_query_rows)
+            and count > 0):
+        raise ValueError("Packed cache split metadata disagree")
+    if (int(packed_old_length) != packed.prefix_total
+            or tuple(int(v) for v in old_lengths) != packed.prefix_lengths
+            or tuple(int(v) for v in cache_offsets) != tuple(
+                np.cumsum([0] + list(packed.prefix_lengths[:-1])).tolist())
+            or not packed.layers):
+        raise ValueError("Packed cache split metadata disagree")
+    rows_total = packed.num_rows
+    row_offset = np.zeros(count + 1, np.int64)
+    row_offset[:count] = np.asarray(query_offsets, np.int64)
+    row_offset[count] = rows_total
+    if (np.diff(row_offset) < 0).any() or row_offset[0] < 0:
+        raise ValueError("Packed cache split metadata disagree")
+    for i, rows in enumerate(keep_query_rows):
+        if any(not 0 <= int(r) < row_offset[i + 1] - row_offset[i] for r in rows):
+            raise ValueError("Packed cache split metadata disagree")
+    sizes = [int(L) + len(k) for L, k in zip(old_lengths, keep_query_rows)]
+    out_offset = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.int64)
+    total = int(sum(sizes))
+    source = packed.prefix_source
+    k0 = source.key_storage[0]
+    hkv, dim = k0.shape[0], k0.shape[2]
+    dev = packed.device
+    out_k = [torch.empty((hkv, total, dim), dtype=k0.dtype, device=dev)
+             for _ in packed.layers]
+    out_v = [torch.empty_like(t) for t in out_k]
+    keep_stride = max(1, max(len(k) for k in keep_query_rows))
+    keep = np.full((count, keep_stride), -1, np.int32)
+    for i, rows in enumerate(keep_query_rows):
+        keep[i, :len(rows)] = [int(r) for r in rows]
+    meta = torch.from_numpy(np.concatenate([
+        np.asarray(packed.prefix_starts, np.int64), out_offset])).to(dev)
+    meta32 = torch.from_numpy(np.concatenate([
+        np.asarray(old_lengths, np.int32), row_offset.astype(np.int32),
+        np.asarray([len(k) for k in keep_query_rows], np.int32), keep.reshape(-1)])).to(dev)
+    kt = packed.layers[0].tree_keys
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    ops.kv_split(
+        ops.pointer_array(source.key_storage[:len(packed.layers)], dev),
+        ops.pointer_array(source.value_storage[:len(packed.layers)], dev),
+        packed.key_pointers(), packed.value_pointers(),
+        ops.pointer_array(out_k, dev), ops.pointer_array(out_v, dev),
+        num_kv_heads=hkv, head_dim=dim,
+        prefix_head_stride=k0.stride(0), prefix_token_stride=k0.stride(1),
+        tree_row_stride=kt.stride(0), tree_head_stride=kt.stride(1),
+        out_head_stride=out_k[0].stride(0), out_token_stride=out_k[0].stride(1),
+        cache_offset=meta[:count], old_length=meta32[:count],
+        row_offset=meta32[count:2 * count + 1], keep_len=meta32[2 * count + 1:3 * count + 1],
+        keep_rows=meta32[3 * count + 1:].view(count, keep_stride),
+        out_offset=meta[count:], max_tokens=max(sizes), status=status)
+    results = []
+    for i in range(count):
+        cache = cache_factory() if cache_factory is not None else RequestCache()
+        a, b = int(out_offset[i]), int(out_offset[i]) + sizes[i]
+        for layer_index in range(len(packed.layers)):
+            cache.update(out_k[layer_index][:, a:b].unsqueeze(0),
+                         out_v[layer_index][:, a:b].unsqueeze(0), layer_index)
+        results.append(cache)
+    return tuple(results)

@@ -15,6 +15,8 @@
 // have read it, so no copy can see a length already advanced.  A kept row
 // outside the request's packed rows leaves the request untouched and reports
 // SG_EINVAL through status.
+#include <algorithm>
+#include <climits>
 #include <type_traits>
 
 #include "sg_common.h"
@@ -216,6 +218,133 @@ extern "C" int sg_kv_commit(const SgKvCommitArgs* args, sg_stream_t stream) {
                      dim3(kCommitThreads), 0, s, a);
   SG_LAUNCH_CHECK();
   hipLaunchKernelGGL(kv_commit_lengths_kernel, dim3(a.num_requests), dim3(64), 0, s, a);
+  SG_LAUNCH_CHECK();
+  return SG_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Non-persistent split: rebuild every request's cache from one packed wave,
+// all layers in one launch (reference _split_compacted_sequence_caches,
+// continuous_tree_block_decode.py:409-450):
+//   out[l][g, o_i + t]       = prefix[l][g, c_i + t]                 t < L_i
+//   out[l][g, o_i + L_i + t] = tree[l][q_i + keep_i[t], g]           t < keep_len_i
+// Grid (token block, request, layer); a workgroup moves the tokens of one
+// block of one request's new cache for one layer (1024 16-byte chunks: 8
+// tokens at 8 kv heads x D 128), four loads in flight per thread.  A kept row
+// outside the request's packed rows is not copied and raises status
+// (SG_EINVAL); so does a request longer than max_tokens.
+// ---------------------------------------------------------------------------
+namespace sg {
+namespace {
+
+constexpr int kSplitThreads = 256;
+constexpr int kSplitChunksPerBlock = kSplitThreads * kCommitBatch;
+
+__global__ __launch_bounds__(kSplitThreads) void kv_split_kernel(SgKvSplitArgs a,
+                                                                 int tokens_per_block) {
+  const int req = blockIdx.y;
+  const int layer = blockIdx.z;
+  const int L = a.old_length_dev[req];
+  const int keep_len = a.keep_len_dev[req];
+  const int r0 = a.row_offset_dev[req];
+  const int rows = a.row_offset_dev[req + 1] - r0;
+  const int64_t c0 = a.cache_offset_dev[req];
+  const int64_t o0 = a.out_offset_dev[req];
+  const int32_t* keep = a.keep_rows_dev + static_cast<int64_t>(a.keep_stride) * req;
+  const int n_out = L + keep_len;
+  if (blockIdx.x == 0 && layer == 0 && threadIdx.x == 0 && a.status_dev != nullptr &&
+      (L < 0 || keep_len < 0 || keep_len > a.keep_stride || n_out > a.max_tokens))
+    atomicExch(a.status_dev, SG_EINVAL);
+  if (L < 0 || keep_len < 0 || keep_len > a.keep_stride || n_out > a.max_tokens) return;
+  const int t_begin = blockIdx.x * tokens_per_block;
+  const int t_end = min(n_out, t_begin + tokens_per_block);
+  if (t_begin >= t_end) return;
+  const uint16_t* k_pre = static_cast<const uint16_t*>(a.k_prefix_layers_dev[layer]);
+  const uint16_t* v_pre = static_cast<const uint16_t*>(a.v_prefix_layers_dev[layer]);
+  const uint16_t* k_tree = static_cast<const uint16_t*>(a.k_tree_layers_dev[layer]);
+  const uint16_t* v_tree = static_cast<const uint16_t*>(a.v_tree_layers_dev[layer]);
+  uint16_t* k_out = static_cast<uint16_t*>(a.k_out_layers_dev[layer]);
+  uint16_t* v_out = static_cast<uint16_t*>(a.v_out_layers_dev[layer]);
+  const int chunks_per_head = a.head_dim / 8;
+  const int chunks_per_token = 2 * a.num_kv_heads * chunks_per_head;  // K then V
+  const int total = (t_end - t_begin) * chunks_per_token;
+  // Chunk idx -> (source, destination); nullptr destination: nothing to do.
+  auto locate = [&](int idx, const GlobalU4*& from, GlobalU4*& to) {
+    from = nullptr;
+    to = nullptr;
+    if (idx >= total) return;
+    const int t = t_begin + idx / chunks_per_token;
+    const int rem = idx % chunks_per_token;
+    const bool is_v = rem >= chunks_per_token / 2;
+    const int c = is_v ? rem - chunks_per_token / 2 : rem;
+    const int g = c / chunks_per_head;
+    const int chunk = c - g * chunks_per_head;
+    if (t < L) {
+      from = (const GlobalU4*)((is_v ? v_pre : k_pre) + g * a.prefix_head_stride +
+                               (c0 + t) * a.prefix_token_stride + chunk * 8);
+    } else {
+      const int k = keep[t - L];
+      if (k < 0 || k >= rows) {
+        if (a.status_dev != nullptr) atomicExch(a.status_dev, SG_EINVAL);
+        return;
+      }
+      from = (const GlobalU4*)((is_v ? v_tree : k_tree) +
+                               static_cast<int64_t>(r0 + k) * a.tree_row_stride +
+                               g * a.tree_head_stride + chunk * 8);
+    }
+    to = (GlobalU4*)((is_v ? v_out : k_out) + g * a.out_head_stride +
+                     (o0 + t) * a.out_token_stride + chunk * 8);
+  };
+  for (int base = threadIdx.x; base < total; base += kSplitChunksPerBlock) {
+    const GlobalU4* f[kCommitBatch];
+    GlobalU4* d[kCommitBatch];
+    u32x4 v[kCommitBatch];
+#pragma unroll
+    for (int j = 0; j < kCommitBatch; ++j) locate(base + j * kSplitThreads, f[j], d[j]);
+#pragma unroll
+    for (int j = 0; j < kCommitBatch; ++j) v[j] = d[j] != nullptr ? *f[j] : u32x4{0, 0, 0, 0};
+    // All four loads complete here, before the conditional stores.
+    asm volatile("" ::"v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]));
+#pragma unroll
+    for (int j = 0; j < kCommitBatch; ++j)
+      if (d[j] != nullptr) *d[j] = v[j];
+  }
+}
+
+}  // namespace
+}  // namespace sg
+
+extern "C" int sg_kv_split(const SgKvSplitArgs* args, sg_stream_t stream) {
+  using namespace sg;
+  clear_error();
+  SG_REQUIRE(args != nullptr, "null SgKvSplitArgs");
+  const SgKvSplitArgs& a = *args;
+  SG_REQUIRE(a.num_layers >= 0 && a.num_requests >= 0 && a.max_tokens >= 0, "negative sizes");
+  if (a.num_layers == 0 || a.num_requests == 0 || a.max_tokens == 0) return SG_OK;
+  SG_REQUIRE(a.num_kv_heads >= 1 && a.head_dim >= 8 && a.head_dim % 8 == 0,
+             "head_dim must be a positive multiple of 8");
+  SG_REQUIRE(a.keep_stride >= 1, "keep_stride must be positive");
+  SG_REQUIRE(a.prefix_head_stride % 8 == 0 && a.prefix_token_stride % 8 == 0 &&
+                 a.tree_row_stride % 8 == 0 && a.tree_head_stride % 8 == 0 &&
+                 a.out_head_stride % 8 == 0 && a.out_token_stride % 8 == 0,
+             "strides must be multiples of 8 elements (16-byte rows)");
+  SG_REQUIRE(a.k_prefix_layers_dev && a.v_prefix_layers_dev && a.k_tree_layers_dev &&
+                 a.v_tree_layers_dev && a.k_out_layers_dev && a.v_out_layers_dev &&
+                 a.cache_offset_dev && a.old_length_dev && a.row_offset_dev &&
+                 a.keep_rows_dev && a.keep_len_dev && a.out_offset_dev,
+             "null device pointer");
+  SG_REQUIRE(a.num_requests <= 65535 && a.num_layers <= 65535,
+             "at most 65535 requests and layers per call");
+  const int chunks_per_token = 2 * a.num_kv_heads * (a.head_dim / 8);
+  SG_REQUIRE(chunks_per_token <= (1 << 20), "num_kv_heads * head_dim too large");
+  const int tokens_per_block = std::max(1, kSplitChunksPerBlock / chunks_per_token);
+  const int64_t blocks = (static_cast<int64_t>(a.max_tokens) + tokens_per_block - 1) /
+                         tokens_per_block;
+  SG_REQUIRE(blocks <= INT32_MAX, "max_tokens too large");
+  hipLaunchKernelGGL(kv_split_kernel,
+                     dim3(static_cast<unsigned>(blocks), a.num_requests, a.num_layers),
+                     dim3(kSplitThreads), 0, reinterpret_cast<hipStream_t>(stream), a,
+                     tokens_per_block);
   SG_LAUNCH_CHECK();
   return SG_OK;
 }

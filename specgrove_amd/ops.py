@@ -295,6 +295,67 @@ def kv_commit(k_cache_ptrs: torch.Tensor, v_cache_ptrs: torch.Tensor,
     _lib.check(_lib.load().sg_kv_commit(ctypes.byref(a), _stream_handle()), "sg_kv_commit")
 
 
+def kv_split(k_prefix_ptrs: torch.Tensor, v_prefix_ptrs: torch.Tensor,
+             k_tree_ptrs: torch.Tensor, v_tree_ptrs: torch.Tensor,
+             k_out_ptrs: torch.Tensor, v_out_ptrs: torch.Tensor, *,
+             num_kv_heads: int, head_dim: int, prefix_head_stride: int,
+             prefix_token_stride: int, tree_row_stride: int, tree_head_stride: int,
+             out_head_stride: int, out_token_stride: int, cache_offset: torch.Tensor,
+             old_length: torch.Tensor, row_offset: torch.Tensor, keep_rows: torch.Tensor,
+             keep_len: torch.Tensor, out_offset: torch.Tensor, max_tokens: int,
+             status: torch.Tensor | None = None) -> None:
+    """Rebuild every request's cache (old prefix + kept rows) from one packed
+    wave, all layers in one call (the non-persistent split).
+
+    ``*_ptrs`` are int64 device arrays of per-layer bases (see pointer_array);
+    cache_offset/out_offset [n] i64, old_length/keep_len [n] i32, row_offset
+    [n+1] i32, keep_rows [n, keep_stride] i32.
+    """
+    for t, name in ((k_prefix_ptrs, "k_prefix_ptrs"), (v_prefix_ptrs, "v_prefix_ptrs"),
+                    (k_tree_ptrs, "k_tree_ptrs"), (v_tree_ptrs, "v_tree_ptrs"),
+                    (k_out_ptrs, "k_out_ptrs"), (v_out_ptrs, "v_out_ptrs"),
+                    (cache_offset, "cache_offset"), (out_offset, "out_offset")):
+        _check_device_tensor(t, name, torch.int64)
+    for t, name in ((old_length, "old_length"), (row_offset, "row_offset"),
+                    (keep_rows, "keep_rows"), (keep_len, "keep_len")):
+        _check_device_tensor(t, name, torch.int32)
+    layers = k_prefix_ptrs.numel()
+    _require(all(t.numel() == layers for t in (v_prefix_ptrs, k_tree_ptrs, v_tree_ptrs,
+                                               k_out_ptrs, v_out_ptrs)),
+             "per-layer pointer arrays disagree")
+    _require(keep_rows.dim() == 2 and keep_rows.is_contiguous(), "keep_rows must be [n, stride]")
+    n = keep_rows.shape[0]
+    _require(cache_offset.numel() == n and out_offset.numel() == n and old_length.numel() == n
+             and keep_len.numel() == n and row_offset.numel() == n + 1,
+             "request metadata sizes disagree")
+    if status is not None:
+        _check_device_tensor(status, "status", torch.int32)
+    a = _lib.SgKvSplitArgs()
+    a.num_layers = layers
+    a.num_requests = n
+    a.num_kv_heads = num_kv_heads
+    a.head_dim = head_dim
+    a.max_tokens = max_tokens
+    a.keep_stride = keep_rows.shape[1]
+    a.k_prefix_layers_dev = k_prefix_ptrs.data_ptr()
+    a.v_prefix_layers_dev = v_prefix_ptrs.data_ptr()
+    a.prefix_head_stride, a.prefix_token_stride = prefix_head_stride, prefix_token_stride
+    a.k_tree_layers_dev = k_tree_ptrs.data_ptr()
+    a.v_tree_layers_dev = v_tree_ptrs.data_ptr()
+    a.tree_row_stride, a.tree_head_stride = tree_row_stride, tree_head_stride
+    a.k_out_layers_dev = k_out_ptrs.data_ptr()
+    a.v_out_layers_dev = v_out_ptrs.data_ptr()
+    a.out_head_stride, a.out_token_stride = out_head_stride, out_token_stride
+    a.cache_offset_dev = cache_offset.data_ptr()
+    a.old_length_dev = old_length.data_ptr()
+    a.row_offset_dev = row_offset.data_ptr()
+    a.keep_rows_dev = keep_rows.data_ptr()
+    a.keep_len_dev = keep_len.data_ptr()
+    a.out_offset_dev = out_offset.data_ptr()
+    a.status_dev = status.data_ptr() if status is not None else 0
+    _lib.check(_lib.load().sg_kv_split(ctypes.byref(a), _stream_handle()), "sg_kv_split")
+
+
 # --------------------------------------------------------------------------
 # (C) tree sampling
 # --------------------------------------------------------------------------

@@ -203,3 +203,70 @@ def test_commit_overflow_with_several_layers_reports_erange(device, oracle):
     np.testing.assert_array_equal(lengths_dev.cpu().numpy(), olen)
     assert np.array_equal(dk.cpu().view(torch.int16).numpy(), ok)
     assert np.array_equal(dv.cpu().view(torch.int16).numpy(), ov)
+
+
+def _split_case(device, oracle, wl, layers, seed, keep_lists, bad_row=False):
+    """sg_kv_split over ``layers`` layers of the packed prefixes of ``wl``
+    against oracle.kv_split, bit for bit (bf16 moved as 16-bit words)."""
+    from specgrove_amd.ops import kv_split, pointer_array
+    g = torch.Generator().manual_seed(seed)
+    n, hkv, d = wl.num_requests, wl.num_kv_heads, wl.head_dim
+    lengths = [int(v) for v in wl.prefix_len]
+    P = sum(lengths)
+    rows = wl.total_rows
+    prefix_k = torch.randint(-30000, 30000, (layers, hkv, P, d), generator=g, dtype=torch.int16)
+    prefix_v = torch.randint(-30000, 30000, (layers, hkv, P, d), generator=g, dtype=torch.int16)
+    tree_k = torch.randint(-30000, 30000, (layers, rows, hkv, d), generator=g, dtype=torch.int16)
+    tree_v = torch.randint(-30000, 30000, (layers, rows, hkv, d), generator=g, dtype=torch.int16)
+    offsets = np.concatenate([[0], np.cumsum(lengths)[:-1]]).astype(np.int64)
+    sizes = [L + len(k) for L, k in zip(lengths, keep_lists)]
+    out_off = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.int64)
+    T = int(sum(sizes))
+    dev = [t.to(device) for t in (prefix_k, prefix_v, tree_k, tree_v)]
+    out_k = torch.zeros((layers, hkv, T, d), dtype=torch.int16, device=device)
+    out_v = torch.zeros_like(out_k)
+    width = max(1, max(len(k) for k in keep_lists))
+    keep = np.full((n, width), -1, np.int32)
+    for i, k in enumerate(keep_lists):
+        keep[i, :len(k)] = k
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    ptr = lambda t: pointer_array([t[l] for l in range(layers)], device)  # noqa: E731
+    kv_split(ptr(dev[0]), ptr(dev[1]), ptr(dev[2]), ptr(dev[3]), ptr(out_k), ptr(out_v),
+             num_kv_heads=hkv, head_dim=d, prefix_head_stride=P * d, prefix_token_stride=d,
+             tree_row_stride=hkv * d, tree_head_stride=d, out_head_stride=T * d,
+             out_token_stride=d, cache_offset=torch.from_numpy(offsets).to(device),
+             old_length=torch.tensor(lengths, dtype=torch.int32, device=device),
+             row_offset=torch.from_numpy(wl.row_offset).to(device),
+             keep_rows=torch.from_numpy(keep).to(device),
+             keep_len=torch.tensor([len(k) for k in keep_lists], dtype=torch.int32,
+                                   device=device),
+             out_offset=torch.from_numpy(out_off).to(device), max_tokens=max(sizes),
+             status=status)
+    torch.cuda.synchronize()
+    got_k, got_v = out_k.cpu().numpy(), out_v.cpu().numpy()
+    if bad_row:
+        return int(status.item()), got_k
+    assert int(status.item()) == 0
+    want = oracle.kv_split(prefix_k.numpy(), prefix_v.numpy(), tree_k.numpy(), tree_v.numpy(),
+                           offsets, lengths, wl.row_offset, keep_lists)
+    for i, (wk, wv) in enumerate(want):
+        a, b = int(out_off[i]), int(out_off[i]) + sizes[i]
+        assert np.array_equal(got_k[:, :, a:b], wk) and np.array_equal(got_v[:, :, a:b], wv), i
+
+
+def test_split_qwen3_4b_shape_bit_exact(device, oracle):
+    """The non-persistent split of the Qwen3-4B-shape wave (16 requests,
+    prefixes U{256..2048}), 3 layers, kept paths of 1-9 rows."""
+    wl = W.qwen3_4b_workload()
+    _split_case(device, oracle, wl, 3, 5, wl.keep)
+
+
+def test_split_fixture_and_edge_cases(device, oracle):
+    """Empty keep lists, a request with an empty prefix, head dim 64, and a
+    kept row outside its request (not copied, status EINVAL)."""
+    wl = W.tiny_attention_workload(seed=4, num_q_heads=4, num_kv_heads=2, head_dim=64)
+    wl.prefix_len[1] = 0
+    keeps = [[0, 3, 5], [], [0], [0, 1, 2, 3, 4, 5, 6, 7, 8]]
+    _split_case(device, oracle, wl, 2, 6, keeps)
+    status, _ = _split_case(device, oracle, wl, 2, 6, [[0, 99], [0], [0], [0]], bad_row=True)
+    assert status == -1

@@ -180,3 +180,45 @@ def test_transformers_routes_every_layer_to_the_plug():
         attention.register()
     assert seen == [(0, (1, 4, 5, 64), (1, 2, 5, 64), True)]
     assert len(packed.layers) == 1 and packed.layers[0].keys.shape == (1, 2, 5, 64)
+
+
+def test_non_persistent_pack_concatenates_in_requested_order():
+    """pack_cache_sequence on plain request caches builds one packed prefix
+    per layer in the requested order (the reference's pack-order fixture,
+    test_continuous_tree_block_decode.py:248-267) and pack_block_inputs finds
+    it through the request caches."""
+    from specgrove_amd.cache import PackedPrefix
+    first = torch.tensor([1, 2], dtype=torch.float32).reshape(1, 1, 2, 1)
+    second = torch.tensor([3, 4, 5], dtype=torch.float32).reshape(1, 1, 3, 1)
+    caches = [_Cache([_Layer(first, -first)]), _Cache([_Layer(second, -second)])]
+    packed, lengths, offsets, total = pack_cache_sequence(tuple(reversed(caches)))
+    assert lengths == (3, 2) and offsets == (0, 3) and total == 5
+    assert isinstance(packed.prefix_source, PackedPrefix) and packed.pool is None
+    assert packed.prefix_source.key_storage[0].flatten().tolist() == [3, 4, 5, 1, 2]
+    assert packed.prefix_source.value_storage[0].flatten().tolist() == [-3, -4, -5, -1, -2]
+    states = [SimpleNamespace(generated=[7], block_root=0, tree=None, round_prefix_len=L,
+                              target_cache=c) for c, L in zip(reversed(caches), (3, 2))]
+    blocks = [SimpleNamespace(nodes=[0, 1], parents=[-1, 0], tokens=[9], depths=[0, 1])] * 2
+    ids, positions, mask, qoff = attention.pack_block_inputs(
+        states, blocks, lengths, offsets, total, torch.float32, "cpu")
+    assert mask["full_attention"].prefix_start.tolist() == [0, 3]
+    assert mask["full_attention"].prefix_len.tolist() == [3, 2]
+    with pytest.raises(ValueError, match="packed together"):
+        attention.pack_block_inputs(states[:1], blocks[:1], lengths[:1], offsets[:1], 3,
+                                    torch.float32, "cpu")
+
+
+def test_non_persistent_split_validates_like_the_reference():
+    from specgrove_amd.cache import split_compacted_sequence_caches
+    first = torch.zeros((1, 1, 2, 8))
+    second = torch.zeros((1, 1, 3, 8))
+    caches = [_Cache([_Layer(first, first)]), _Cache([_Layer(second, second)])]
+    packed, lengths, offsets, total = pack_cache_sequence(caches)
+    packed.update(torch.zeros((1, 1, 5, 8)), torch.zeros((1, 1, 5, 8)), 0)
+    for args in (((0, 2), (2, 3), 5, (0, 3), ((0, 2),)),          # fewer keep lists
+                 ((0, 2), (2, 3), 6, (0, 3), ((0, 2), (1,))),     # wrong packed length
+                 ((0, 1), (2, 3), 5, (0, 3), ((0, 2), (1,))),     # wrong offsets
+                 ((0, 2), (2, 3), 5, (0, 3), ((0, 3), (1,)))):    # row outside request 0
+        with pytest.raises(ValueError, match="split metadata disagree"):
+            split_compacted_sequence_caches(packed, None, args[0], args[1], args[2], args[3],
+                                            args[4], "cpu")

@@ -39,6 +39,22 @@ def test_continuation_positions(oracle):
     assert positions.tolist() == fx["positions"]
 
 
+def test_bulk_split_fixture(oracle):
+    """oracle.kv_split reproduces the reference's bulk split fixture exactly
+    (keys and values of both requests)."""
+    fx = FX["bulk_split"]
+    packed = np.asarray(fx["packed_keys"], np.float64)
+    P = fx["packed_old_length"]
+    prefix = packed[:P].reshape(1, 1, P, 1)
+    tree = packed[P:].reshape(1, -1, 1, 1)
+    row_offset = fx["query_offsets"] + [tree.shape[1]]
+    out = oracle.kv_split(prefix, -prefix, tree, -tree, fx["cache_offsets"],
+                          fx["old_lengths"], row_offset, fx["keep_query_rows"])
+    for i, (keys, values) in enumerate(out):
+        assert keys.reshape(-1).tolist() == fx["keys"][i]
+        assert values.reshape(-1).tolist() == fx["values"][i]
+
+
 def test_bulk_split_fixture_via_commit(oracle):
     """Old prefix rows + kept query rows == the reference's split fixture."""
     fx = FX["bulk_split"]
