@@ -220,3 +220,31 @@ def test_stated_tiny_workload(device, oracle):
     res, waves, _ = _decode((gpu_model, cpu_model, prompts), device, oracle, persistent=True,
                             drafter=_RandomDrafter(13), max_new=4, row_cap=16, row_budget=64)
     assert waves[0][0] == [16, 16, 16, 16] and all(sum(sizes) <= 64 for sizes, _ in waves)
+
+
+def test_open_loop_serving(peaked, device, oracle):
+    """Six requests arriving over 40 ms, at most three active: the serving
+    wrapper admits them at wave boundaries, prefills newcomers, runs the
+    non-persistent wave loop and reports per-request latencies."""
+    from specgrove_amd import decode, serving
+    gpu_model, cpu_model, prompts = peaked
+    prompts = prompts + prompts[:2]
+    drafter = _Drafter(cpu_model, prompts)
+    states = [decode.DecodeRequest(i, [], None, torch.Generator(device).manual_seed(90 + i))
+              for i in range(len(prompts))]
+
+    def prefill(new):
+        caches, anchors = _prefill(cpu_model, [prompts[s.request_id] for s in new], device)
+        for s, c, a in zip(new, caches, anchors):
+            s.target_cache, s.generated = c, [a]
+
+    arrivals = [0.0, 0.0, 0.005, 0.01, 0.02, 0.04]
+    res = serving.serve_open_loop(gpu_model, states, arrivals, drafter, prefill,
+                                  max_active_requests=3, max_new_tokens=10, row_cap=16)
+    assert res.max_concurrent <= 3
+    for s, m in zip(states, res.request_metrics):
+        assert s.done and 1 <= len(s.generated) <= 10 and m["output_tokens"] == len(s.generated)
+        assert 0 <= m["queue_ms"] <= m["ttft_ms"] <= m["e2e_ms"]
+        assert m["arrival_ms"] <= m["admitted_ms"]
+    print("metrics", [(round(m["ttft_ms"], 1), round(m["tpot_ms"], 2))
+                      for m in res.request_metrics], flush=True)
