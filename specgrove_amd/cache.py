@@ -81,8 +81,12 @@ class PersistentRequestCachePool:
 
     ``caches`` are per-request caches holding one request each (a transformers
     ``DynamicCache`` after prefill, or anything with ``layers[l].keys/values``
-    of shape [1, Hkv, L, D]).  Besides the host ``lengths`` list, the pool
-    keeps device copies of the lengths and slot offsets for the kernels.
+    of shape [1, Hkv, L, D]).  The arena of every layer is one slice of a
+    single ``[2, layers, Hkv, slots * capacity, D]`` allocation (K then V), so
+    the per-layer ``key_storage[l]`` / ``value_storage[l]`` views the reference
+    exposes are contiguous and the kernels get one pointer per layer; each
+    request's prefill is copied in with one stacked copy over all its layers.
+    ``lengths`` (host) are the cached lengths per slot.
     """
 
     def __init__(self, caches: Sequence, capacity: int):
@@ -91,29 +95,27 @@ class PersistentRequestCachePool:
         lengths = [_cache_length(cache) for cache in caches]
         if capacity < max(lengths):
             raise ValueError("Persistent cache capacity is below the prefix")
-        layer_count = len(caches[0].layers)
-        if any(len(cache.layers) != layer_count for cache in caches):
+        layers = len(caches[0].layers)
+        if any(len(cache.layers) != layers for cache in caches):
             raise ValueError("Target caches have different layer counts")
+        first = caches[0].layers
+        if any(layer.keys.shape[0] != 1 for cache in caches for layer in cache.layers):
+            raise ValueError("Expected one request per source cache")
+        hkv, dim = first[0].keys.shape[1], first[0].keys.shape[-1]
         self.capacity = int(capacity)
         self.lengths = list(lengths)
-        self.key_storage: list[torch.Tensor] = []
-        self.value_storage: list[torch.Tensor] = []
-        for layer_index in range(layer_count):
-            example = caches[0].layers[layer_index]
-            if example.keys.shape[0] != 1:
-                raise ValueError("Expected one request per source cache")
-            shape = (example.keys.shape[1], len(caches) * self.capacity, example.keys.shape[-1])
-            keys = torch.empty(shape, dtype=example.keys.dtype, device=example.keys.device)
-            values = torch.empty(shape, dtype=example.values.dtype,
-                                 device=example.values.device)
-            for slot, (cache, length) in enumerate(zip(caches, lengths)):
-                source = cache.layers[layer_index]
-                start = slot * self.capacity
-                keys[:, start:start + length].copy_(source.keys[0])
-                values[:, start:start + length].copy_(source.values[0])
-            self.key_storage.append(keys)
-            self.value_storage.append(values)
-        self.device = self.key_storage[0].device
+        arena = torch.empty((2, layers, hkv, len(caches) * self.capacity, dim),
+                            dtype=first[0].keys.dtype, device=first[0].keys.device)
+        for slot, (cache, length) in enumerate(zip(caches, lengths)):
+            if length == 0:
+                continue
+            at = slice(slot * self.capacity, slot * self.capacity + length)
+            arena[0, :, :, at] = torch.stack([layer.keys[0] for layer in cache.layers])
+            arena[1, :, :, at] = torch.stack([layer.values[0] for layer in cache.layers])
+        self._arena = arena
+        self.key_storage: list[torch.Tensor] = list(arena[0].unbind(0))
+        self.value_storage: list[torch.Tensor] = list(arena[1].unbind(0))
+        self.device = arena.device
         self.caches = tuple(PersistentRequestCache(self, slot) for slot in range(len(caches)))
         self._k_ptrs = None
         self._v_ptrs = None
