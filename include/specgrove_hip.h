@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define SG_ABI_VERSION 3
+#define SG_ABI_VERSION 4
 
 #define SG_OK 0
 #define SG_EINVAL (-1)  /* shape or contract violation (Python: ValueError) */
@@ -251,7 +251,24 @@ typedef struct SgTreeSampleArgs {
                                     and per-line complement totals of the exit rows,
                                     and each request's exit node and its children */
   size_t workspace_bytes;
+  /* Lazy projection (FTS:2840-3019, SMP:738-832): only the rows a walk can
+   * route from were projected (sg_lm_head below). */
+  const int32_t* logits_row_dev; /* optional [num_rows]: logits row of each packed
+                                    node, or -1 when the node was not projected,
+                                    which only a node without children may be;
+                                    NULL: node r reads logits row r */
+  int32_t num_logits_rows;       /* rows of logits, row_max and row_sum; 0 means
+                                    num_rows */
+  int32_t flags;                 /* SG_SAMPLE_STATS_READY: row_max/row_sum already
+                                    hold every logits row's statistics (as
+                                    sg_lm_head writes them); no statistics pass */
+  int32_t* terminal_leaf_dev;    /* optional [n]: the walk's last node when its row
+                                    was not projected -- its bonus is then -1 and
+                                    the caller projects that leaf and draws from it
+                                    (FTS:2965-2989) -- else -1 */
 } SgTreeSampleArgs;
+
+#define SG_SAMPLE_STATS_READY 1
 
 /* Row statistics of all packed rows followed by the per-request walk. */
 int sg_tree_sample(const SgTreeSampleArgs* args, sg_stream_t stream);
@@ -281,9 +298,49 @@ int sg_row_stats(const void* logits_dev, int32_t logits_dtype, int64_t row_strid
                  int32_t vocab, int32_t num_rows, float* row_max_dev, float* row_sum_dev,
                  sg_stream_t stream);
 
+/* ------------------------------------------------------------------------
+ * (D) LM head with fused softmax statistics (lazy projection).
+ *
+ * Replaces lm_head(hidden) + probabilities(...) on the rows a tree walk can
+ * need: the internal rows of every request (FTS:2899-2913) and, in a second
+ * call, the leaves the walks reached (FTS:2974-2984); single-request law
+ * SMP:738-832, call site CTBD:1807-1824.  logits[r] = weight . hidden[row_index[r]]
+ * in fp32 over bf16 inputs, rounded to bf16 (nearest even).  From the rounded
+ * logits: per 128-token tile t of row r, (max, sum of E(x - max)) in
+ * tile_stats[r][t], and the row's (max, sum) in row_max/row_sum, which
+ * sg_tree_sample takes with SG_SAMPLE_STATS_READY.  Summation order: tile
+ * tokens 128t + 32b + 8q + 4h + e form half h, summed in increasing (b, q, e),
+ * z = z_0 + z_1; tiles merge into lane t % 64 in increasing t, then an xor
+ * butterfly over the 64 lanes.
+ * ---------------------------------------------------------------------- */
+typedef struct SgLmHeadArgs {
+  int32_t num_rows;              /* Rp >= 0 rows to project */
+  int32_t hidden_size;           /* H, a positive multiple of 32 */
+  int32_t vocab;                 /* V >= 1 */
+  int32_t num_hidden_rows;       /* rows of hidden_dev (row_index range) */
+  const void* hidden_dev;        /* bf16 [num_hidden_rows, hidden_row_stride], < 4 GiB */
+  int64_t hidden_row_stride;     /* elements, multiple of 8 */
+  const int32_t* row_index_dev;  /* optional [Rp]: hidden row of projected row r;
+                                    NULL: row r */
+  const void* weight_dev;        /* bf16 [V, weight_row_stride] (lm_head.weight) */
+  int64_t weight_row_stride;     /* elements, multiple of 8 */
+  void* logits_dev;              /* bf16 [Rp, logits_row_stride] output */
+  int64_t logits_row_stride;     /* elements, multiple of 8, >= V */
+  float* tile_stats_dev;         /* [Rp, sg_lm_head_tile_count(V), 2] output */
+  float* row_max_dev;            /* [Rp] output */
+  float* row_sum_dev;            /* [Rp] output */
+  int32_t* status_dev;           /* optional [1]: SG_EINVAL when a row index lies
+                                    outside [0, num_hidden_rows); never cleared */
+} SgLmHeadArgs;
+
+int sg_lm_head(const SgLmHeadArgs* args, sg_stream_t stream);
+
+/* 128-token statistics tiles per row: ceil(V / 128), or -1 for V < 1. */
+int64_t sg_lm_head_tile_count(int32_t vocab);
+
 /* sizeof() of the argument structs as compiled into the library, for binding
  * checks: which = 0 SgTreeAttnArgs, 1 SgKvCommitArgs, 2 SgTreeSampleArgs,
- * 3 SgKvSplitArgs.
+ * 3 SgKvSplitArgs, 4 SgLmHeadArgs.
  * Returns -1 for an unknown index.  No reference counterpart. */
 int64_t sg_abi_struct_size(int32_t which);
 

@@ -18,7 +18,10 @@ Parts:
                 of CTBD:2108-2109;
   * sampling -- ctypes binding of sg_oracle.c (explicit-uniform tree rejection
                 sampler, law of sampling.py:903-950) plus the ancestral walk of
-                sampling.py:937-950 on pre-drawn posterior tokens.
+                sampling.py:937-950 on pre-drawn posterior tokens;
+  * LM head  -- the statistics epilogue of the lazy projection and the walk
+                over a partly projected wave (fused_tree_sampling.py:2840-3019,
+                sampling.py:738-832), also in sg_oracle.c.
 """
 from __future__ import annotations
 
@@ -67,6 +70,16 @@ def lib() -> ctypes.CDLL:
             i32p, f32p, ctypes.c_int32, ctypes.c_int32, i32p, i32p, i32p,
             f32p, f32p,
         ]
+        handle.sgo_tree_sample_mapped.restype = ctypes.c_int
+        handle.sgo_tree_sample_mapped.argtypes = [
+            f32p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, i32p, i32p,
+            i32p, f32p, ctypes.c_int32, ctypes.c_int32, i32p, f32p, f32p,
+            i32p, i32p, i32p, i32p,
+        ]
+        handle.sgo_lm_head_tile_stats.restype = None
+        handle.sgo_lm_head_tile_stats.argtypes = [f32p, ctypes.c_int64, f32p]
+        handle.sgo_lm_head_row_stats.restype = None
+        handle.sgo_lm_head_row_stats.argtypes = [f32p, ctypes.c_int64, f32p, f32p]
         _lib = handle
     return _lib
 
@@ -158,6 +171,92 @@ def tree_sample(logits: np.ndarray, row_offset: np.ndarray, parent: np.ndarray,
     if any(status != 0 for status in statuses):
         raise ValueError("oracle sampler rejected its inputs")
     return nodes[:, :max_depth], length, bonus, row_m, row_z
+
+
+def _parallel(count: int, threads: int, fn) -> None:
+    """fn(a, b) over contiguous index ranges (ctypes releases the GIL)."""
+    if count <= 0:
+        return
+    if threads > 1 and count > 1:
+        from concurrent.futures import ThreadPoolExecutor
+        bounds = np.linspace(0, count, min(threads, count) + 1).astype(int)
+        with ThreadPoolExecutor(len(bounds) - 1) as pool:
+            list(pool.map(fn, bounds[:-1], bounds[1:]))
+    else:
+        fn(0, count)
+
+
+def lm_head_stats(logits: np.ndarray, threads: int = 1):
+    """Statistics of the LM head's epilogue for fp32 rows ``logits`` [rows, V]
+    (the bf16 logits the kernel wrote, widened): per-row 128-token tile pairs
+    [rows, ceil(V/128), 2] and the merged row max / sum (sg_oracle.c:
+    sgo_lm_head_tile_stats, sgo_lm_head_row_stats)."""
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    rows, vocab = logits.shape
+    tiles = (vocab + 127) // 128
+    pairs = np.zeros((rows, tiles, 2), np.float32)
+    row_m = np.zeros(rows, np.float32)
+    row_z = np.zeros(rows, np.float32)
+
+    def run(a: int, b: int) -> None:
+        for r in range(a, b):
+            lib().sgo_lm_head_tile_stats(_f32p(logits[r]), vocab, _f32p(pairs[r]))
+            lib().sgo_lm_head_row_stats(_f32p(pairs[r]), tiles, _f32p(row_m[r:r + 1]),
+                                        _f32p(row_z[r:r + 1]))
+    _parallel(rows, threads, run)
+    return pairs, row_m, row_z
+
+
+def tree_sample_mapped(logits: np.ndarray, row_offset: np.ndarray, parent: np.ndarray,
+                       token: np.ndarray, uniforms: np.ndarray, max_depth: int,
+                       row_map: np.ndarray | None, row_m: np.ndarray | None,
+                       row_z: np.ndarray | None, threads: int = 1):
+    """Oracle of the sampler over a partly projected wave.
+
+    ``logits`` [logits rows, V] fp32; ``row_map`` [rows] gives each packed
+    node's logits row (-1: not projected, only for nodes without children;
+    None: row r); ``row_m``/``row_z`` [logits rows] are given statistics (the
+    LM head's) or None (computed as the sampler's own pass does).  Returns
+    (accept_nodes [n, max_depth], accept_len [n], bonus [n], terminal_leaf [n]);
+    bonus is -1 where the walk ended at an unprojected leaf.
+    """
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    row_offset = np.ascontiguousarray(row_offset, dtype=np.int32)
+    parent = np.ascontiguousarray(parent, dtype=np.int32)
+    token = np.ascontiguousarray(token, dtype=np.int32)
+    uniforms = np.ascontiguousarray(uniforms, dtype=np.float32)
+    n = row_offset.size - 1
+    rows = int(row_offset[-1])
+    vocab = logits.shape[1]
+    if row_map is None:
+        row_map = np.arange(rows, dtype=np.int32)
+    row_map = np.ascontiguousarray(row_map, dtype=np.int32)
+    if row_map.size != rows or row_map.max(initial=-1) >= logits.shape[0]:
+        raise ValueError("row map does not fit the logits")
+    given = row_m is not None and row_z is not None
+    if given:
+        row_m = np.ascontiguousarray(row_m, dtype=np.float32)
+        row_z = np.ascontiguousarray(row_z, dtype=np.float32)
+    depth_slots = max(int(max_depth), 1)
+    nodes = np.full((n, depth_slots), -1, np.int32)
+    length = np.zeros(n, np.int32)
+    bonus = np.zeros(n, np.int32)
+    leaf = np.full(n, -1, np.int32)
+    statuses = []
+
+    def run(a: int, b: int) -> None:
+        r0, r1 = int(row_offset[a]), int(row_offset[b])
+        ro = np.ascontiguousarray(row_offset[a:b + 1] - r0)
+        statuses.append(lib().sgo_tree_sample_mapped(
+            _f32p(logits), vocab, vocab, b - a, _i32p(ro),
+            _i32p(parent[r0:r1]), _i32p(token[r0:r1]), _f32p(uniforms[a:b]),
+            uniforms.shape[1], int(max_depth), _i32p(row_map[r0:r1]),
+            _f32p(row_m) if given else None, _f32p(row_z) if given else None,
+            _i32p(nodes[a:b]), _i32p(length[a:b]), _i32p(bonus[a:b]), _i32p(leaf[a:b])))
+    _parallel(n, threads, run)
+    if any(status != 0 for status in statuses):
+        raise ValueError("oracle sampler rejected its inputs")
+    return nodes[:, :max_depth], length, bonus, leaf
 
 
 def ancestral_walk(parents: Sequence[int], tokens: Sequence[int],

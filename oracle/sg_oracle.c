@@ -251,44 +251,43 @@ int32_t sgo_complement_draw(const float* x, int64_t vocab, float m,
 
 /*
  * Sample every request of a packed wave.
- *   logits      [rows, row_stride] fp32 (only the first vocab entries used)
+ *   logits      [logits rows, row_stride] fp32 (only the first vocab entries used)
  *   row_offset  [n+1]   packed row range of request i
  *   parent      [rows]  request-local parent index, -1 for each request's root
  *   token       [rows]  draft token of each node (ignored for roots)
  *   uniforms    [n, uniform_stride] fp32, u[2d] routes and u[2d+1] exits at depth d
  *   max_depth   accept_nodes holds max_depth entries per request
+ *   row_map     optional [rows]: logits row of each packed node, -1 when the node
+ *               was not projected (then it must have no children); NULL: row r
+ *   row_m_in, row_z_in  optional [logits rows]: given row statistics (the LM
+ *               head's); NULL: computed by sgo_row_stats
  * Outputs: accept_nodes [n, max_depth] (local node ids, -1 padded),
- *          accept_len [n], bonus [n], row_m / row_z [rows] (may be NULL).
+ *          accept_len [n], bonus [n] (-1 at an unprojected terminal leaf),
+ *          terminal_leaf [n] (may be NULL: that leaf's local id, else -1).
  * Returns SGO_OK or SGO_EINVAL.
  */
-int sgo_tree_sample(const float* logits, int64_t row_stride, int64_t vocab,
-                    int32_t num_requests, const int32_t* row_offset,
-                    const int32_t* parent, const int32_t* token,
-                    const float* uniforms, int32_t uniform_stride,
-                    int32_t max_depth, int32_t* accept_nodes,
-                    int32_t* accept_len, int32_t* bonus, float* row_m,
-                    float* row_z) {
+int sgo_tree_sample_mapped(const float* logits, int64_t row_stride, int64_t vocab,
+                           int32_t num_requests, const int32_t* row_offset,
+                           const int32_t* parent, const int32_t* token,
+                           const float* uniforms, int32_t uniform_stride,
+                           int32_t max_depth, const int32_t* row_map,
+                           const float* row_m_in, const float* row_z_in,
+                           int32_t* accept_nodes, int32_t* accept_len, int32_t* bonus,
+                           int32_t* terminal_leaf) {
   if (num_requests < 0 || vocab < 1 || max_depth < 0) return SGO_EINVAL;
-  const int32_t rows = row_offset[num_requests];
-  for (int32_t r = 0; r < rows; ++r) {
-    float m, z;
-    sgo_row_stats(logits + (int64_t)r * row_stride, vocab, &m, &z);
-    if (row_m) row_m[r] = m;
-    if (row_z) row_z[r] = z;
-  }
   for (int32_t i = 0; i < num_requests; ++i) {
     const int32_t r0 = row_offset[i];
     const int32_t n = row_offset[i + 1] - r0;
     const float* u = uniforms + (int64_t)i * uniform_stride;
     for (int32_t k = 0; k < max_depth; ++k) accept_nodes[(int64_t)i * max_depth + k] = -1;
+    if (terminal_leaf) terminal_leaf[i] = -1;
     int32_t v = 0, depth = 0;
     int32_t children[1024];
     int32_t child_tokens[1024];
+    if (n < 1 || n > 1024) return SGO_EINVAL;
     for (;;) {
-      if (2 * depth + 1 >= uniform_stride || n > 1024) return SGO_EINVAL;
-      const float* x = logits + (int64_t)(r0 + v) * row_stride;
-      float m, z;
-      sgo_row_stats(x, vocab, &m, &z);
+      if (2 * depth + 1 >= uniform_stride) return SGO_EINVAL;
+      const int32_t lrow = row_map ? row_map[r0 + v] : r0 + v;
       int count = 0;
       for (int32_t w = v + 1; w < n; ++w) {
         if (parent[r0 + w] == v) {
@@ -296,6 +295,22 @@ int sgo_tree_sample(const float* logits, int64_t row_stride, int64_t vocab,
           child_tokens[count] = token[r0 + w];
           ++count;
         }
+      }
+      if (lrow < 0) {
+        /* Unprojected node: only a leaf may be one; its bonus is drawn later. */
+        if (count > 0) return SGO_EINVAL;
+        accept_len[i] = depth;
+        bonus[i] = -1;
+        if (terminal_leaf) terminal_leaf[i] = v;
+        break;
+      }
+      const float* x = logits + (int64_t)lrow * row_stride;
+      float m, z;
+      if (row_m_in && row_z_in) {
+        m = row_m_in[lrow];
+        z = row_z_in[lrow];
+      } else {
+        sgo_row_stats(x, vocab, &m, &z);
       }
       const float route_threshold = u[2 * depth] * z;
       float cumulative = 0.0f;
@@ -320,6 +335,78 @@ int sgo_tree_sample(const float* logits, int64_t row_stride, int64_t vocab,
     }
   }
   return SGO_OK;
+}
+
+/* The unmapped sampler: every packed row has logits, statistics computed here
+ * (row_m / row_z, when given, receive them). */
+int sgo_tree_sample(const float* logits, int64_t row_stride, int64_t vocab,
+                    int32_t num_requests, const int32_t* row_offset,
+                    const int32_t* parent, const int32_t* token,
+                    const float* uniforms, int32_t uniform_stride,
+                    int32_t max_depth, int32_t* accept_nodes,
+                    int32_t* accept_len, int32_t* bonus, float* row_m,
+                    float* row_z) {
+  if (num_requests < 0 || vocab < 1 || max_depth < 0) return SGO_EINVAL;
+  const int32_t rows = row_offset[num_requests];
+  if (row_m && row_z) {
+    for (int32_t r = 0; r < rows; ++r)
+      sgo_row_stats(logits + (int64_t)r * row_stride, vocab, &row_m[r], &row_z[r]);
+  }
+  return sgo_tree_sample_mapped(logits, row_stride, vocab, num_requests, row_offset, parent,
+                                token, uniforms, uniform_stride, max_depth, 0,
+                                (row_m && row_z) ? row_m : 0, (row_m && row_z) ? row_z : 0,
+                                accept_nodes, accept_len, bonus, 0);
+}
+
+/*
+ * LM-head statistics (the fused epilogue of the HIP projection, restated).
+ * Tile t of a row covers tokens 128t .. 128t+127 below vocab; token
+ * 128t + 32b + 8q + 4h + e (b, q, e in 0..3; h in 0..1) is in half h.
+ *   m_t = max of the tile (-inf for a tile with no token);
+ *   z_h = sequential sum, increasing (b, q, e), of E(x - m_t) over half h;
+ *   z_t = z_0 + z_1.
+ * out_pairs receives (m_t, z_t) for t < ceil(vocab / 128).
+ */
+void sgo_lm_head_tile_stats(const float* x, int64_t vocab, float* out_pairs) {
+  const int64_t tiles = (vocab + 127) / 128;
+  for (int64_t t = 0; t < tiles; ++t) {
+    float m = -INFINITY;
+    for (int64_t k = 128 * t; k < 128 * t + 128 && k < vocab; ++k) m = fmaxf(m, x[k]);
+    const float mc = (m == -INFINITY) ? 0.0f : m;
+    float zh[2] = {0.0f, 0.0f};
+    for (int h = 0; h < 2; ++h)
+      for (int b = 0; b < 4; ++b)
+        for (int q = 0; q < 4; ++q)
+          for (int e = 0; e < 4; ++e) {
+            const int64_t k = 128 * t + 32 * b + 8 * q + 4 * h + e;
+            if (k < vocab) zh[h] = zh[h] + sgo_exp(x[k] - mc);
+          }
+    out_pairs[2 * t] = m;
+    out_pairs[2 * t + 1] = zh[0] + zh[1];
+  }
+}
+
+/* Row (max, sum) from its tile pairs: tile t merged into lane t % 64 in
+ * increasing t, then the xor butterfly (32 .. 1) over the 64 lanes. */
+void sgo_lm_head_row_stats(const float* pairs, int64_t tiles, float* out_m, float* out_z) {
+  sgo_mz lane[SGO_LANES];
+  for (int l = 0; l < SGO_LANES; ++l) {
+    lane[l].m = -INFINITY;
+    lane[l].z = 0.0f;
+  }
+  for (int64_t t = 0; t < tiles; ++t) {
+    sgo_mz p;
+    p.m = pairs[2 * t];
+    p.z = pairs[2 * t + 1];
+    lane[t % SGO_LANES] = sgo_merge(lane[t % SGO_LANES], p);
+  }
+  sgo_mz tmp[SGO_LANES];
+  for (int d = 32; d >= 1; d >>= 1) {
+    for (int l = 0; l < SGO_LANES; ++l) tmp[l] = sgo_merge(lane[l], lane[l ^ d]);
+    memcpy(lane, tmp, sizeof(tmp));
+  }
+  *out_m = lane[0].m;
+  *out_z = lane[0].z;
 }
 
 /* Vectorised E(x) for tests of the exp restatement. */

@@ -16,10 +16,11 @@ SG_EINVAL = -1
 SG_ERANGE = -2
 SG_EHIP = -3
 
-SG_ABI_VERSION = 3
+SG_ABI_VERSION = 4
 SG_DTYPE_F32 = 0
 SG_DTYPE_BF16 = 1
 SG_DTYPE_F16 = 2
+SG_SAMPLE_STATS_READY = 1
 
 c_void_p = ctypes.c_void_p
 c_i32 = ctypes.c_int32
@@ -91,6 +92,21 @@ class SgTreeSampleArgs(ctypes.Structure):
         ("bonus_dev", c_void_p), ("keep_rows_dev", c_void_p),
         ("status_dev", c_void_p),
         ("workspace_dev", c_void_p), ("workspace_bytes", c_size),
+        ("logits_row_dev", c_void_p), ("num_logits_rows", c_i32), ("flags", c_i32),
+        ("terminal_leaf_dev", c_void_p),
+    ]
+
+
+class SgLmHeadArgs(ctypes.Structure):
+    _fields_ = [
+        ("num_rows", c_i32), ("hidden_size", c_i32), ("vocab", c_i32),
+        ("num_hidden_rows", c_i32),
+        ("hidden_dev", c_void_p), ("hidden_row_stride", c_i64),
+        ("row_index_dev", c_void_p),
+        ("weight_dev", c_void_p), ("weight_row_stride", c_i64),
+        ("logits_dev", c_void_p), ("logits_row_stride", c_i64),
+        ("tile_stats_dev", c_void_p), ("row_max_dev", c_void_p), ("row_sum_dev", c_void_p),
+        ("status_dev", c_void_p),
     ]
 
 
@@ -99,6 +115,7 @@ EXPORTED_SYMBOLS = (
     "sg_tree_attn_plan", "sg_tree_attn_fwd", "sg_kv_commit",
     "sg_tree_sample", "sg_tree_sample_workspace_bytes", "sg_row_stats", "sg_exp_probe",
     "sg_tree_sample_noalloc", "sg_tree_attn_plan_check", "sg_kv_split",
+    "sg_lm_head", "sg_lm_head_tile_count",
 )
 
 # Static scratch of sg_tree_sample_noalloc (SG_TREE_SAMPLE_NOALLOC_SCRATCH_BYTES).
@@ -150,6 +167,10 @@ def load() -> ctypes.CDLL:
     lib.sg_row_stats.restype = c_i32
     lib.sg_row_stats.argtypes = [c_void_p, c_i32, c_i64, c_i32, c_i32, c_void_p, c_void_p,
                                  c_void_p]
+    lib.sg_lm_head.restype = c_i32
+    lib.sg_lm_head.argtypes = [ctypes.POINTER(SgLmHeadArgs), c_void_p]
+    lib.sg_lm_head_tile_count.restype = c_i64
+    lib.sg_lm_head_tile_count.argtypes = [c_i32]
     lib.sg_exp_probe.restype = c_i32
     lib.sg_exp_probe.argtypes = [c_void_p, c_void_p, c_i64, c_void_p]
     version = lib.sg_abi_version()
@@ -157,7 +178,8 @@ def load() -> ctypes.CDLL:
         raise RuntimeError(f"ABI mismatch: the library is version {version}, the binding "
                            f"version {SG_ABI_VERSION}; rebuild with `python -m "
                            f"specgrove_amd.build`")
-    expected = {0: SgTreeAttnArgs, 1: SgKvCommitArgs, 2: SgTreeSampleArgs, 3: SgKvSplitArgs}
+    expected = {0: SgTreeAttnArgs, 1: SgKvCommitArgs, 2: SgTreeSampleArgs, 3: SgKvSplitArgs,
+                4: SgLmHeadArgs}
     for which, struct in expected.items():
         size = lib.sg_abi_struct_size(which)
         if size != ctypes.sizeof(struct):

@@ -28,6 +28,7 @@ extern "C" int64_t sg_abi_struct_size(int32_t which) {
     case 1: return static_cast<int64_t>(sizeof(SgKvCommitArgs));
     case 2: return static_cast<int64_t>(sizeof(SgTreeSampleArgs));
     case 3: return static_cast<int64_t>(sizeof(SgKvSplitArgs));
+    case 4: return static_cast<int64_t>(sizeof(SgLmHeadArgs));
     default: return -1;
   }
 }

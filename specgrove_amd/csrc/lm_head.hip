@@ -1,0 +1,404 @@
+// Vocabulary projection of a packed verification wave with fused row
+// statistics (the "lazy projection" LM head).
+//
+// Replaces the reference's `lm_head(hidden)` followed by `probabilities(...)`
+// on the rows the tree walk can need (fused_tree_sampling.py:2899-2913 for the
+// internal rows of every request, :2974-2984 for the reached leaves;
+// sampling.py:738-832 for the single-request law): the wave's hidden rows,
+// gathered by index, are multiplied by the bf16 head weight; the kernel writes
+// the bf16 logits and, from those rounded logits, the softmax statistics that
+// the tree walk routes with, so no separate pass reads the logits to normalise
+// them.
+//
+// Kernel (one 4-wave workgroup per CU, 1 wave per SIMD):
+//   tile      = 256 vocabulary tokens x 256 projected rows; wave w owns the
+//               128 x 128 quarter (tokens 128*(w&1).., rows 128*(w>>1)..);
+//   ring      = four stages of 32 hidden dims: the weight and hidden chunks
+//               move HBM -> LDS with global_load_lds_dwordx4 (no register
+//               staging), three stages ahead of the MFMAs;
+//   product   = C^T = W X^T with v_mfma_f32_32x32x16_bf16 (A = weight rows, B =
+//               hidden rows), so each lane ends with 64 logits of one row per
+//               32-row block, fp32-accumulated over the hidden dims in
+//               ascending 16-dim blocks;
+//   epilogue  = round to bf16 (nearest even), per (row, 128-token tile) the
+//               maximum m and z = sum of E(x - m) (the sampler's exp) in the
+//               order below, and the bf16 logits written as whole 256-byte
+//               row segments through LDS;
+//   grid      = XCD-aware: the row tiles of one vocabulary tile run on one XCD
+//               at the same time, so its L2 serves the weight tile to all of
+//               them.
+// A second small kernel merges each row's tile pairs into (max, sum).
+//
+// Statistics contract (bit-exact with the CPU restatement, fp32, contraction
+// off).  Row r, tile t covers tokens 128*t .. 128*t+127 below V.  Token
+// 128*t + 32*b + 8*q + 4*h + e (b, q, e in 0..3, h in 0..1) belongs to half
+// h.  m_t = max of the tile; z_h = sequential sum, in increasing (b, q, e),
+// of E(x - m_t) over the half's tokens below V; z_t = z_0 + z_1.  Row pair:
+// tile t is merged into lane t % 64 in increasing t, then an xor butterfly
+// (distances 32 .. 1) merges the 64 lanes; merge(a, b) = (M, a.z*E(a.m-M) +
+// b.z*E(b.m-M)) with M = max(a.m, b.m).
+#pragma clang fp contract(off)
+
+#include <algorithm>
+
+#include "sg_common.h"
+#include "sg_math.h"
+
+namespace sg {
+namespace {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(16))) float floatx16;
+
+constexpr int kLmThreads = 256;
+constexpr int kTileV = 256;          // vocabulary tokens per workgroup tile
+constexpr int kTileR = 256;          // projected rows per workgroup tile
+constexpr int kStepK = 32;           // hidden dims per ring stage
+constexpr int kLmStages = 4;
+constexpr int kHalfTile = kTileV * kStepK * 2;  // bytes of one operand per stage (16 KiB)
+constexpr int kKbBytes = kHalfTile / 2;         // one 16-dim block of an operand
+constexpr int kStatTokens = 128;     // tokens per statistics tile
+constexpr int kOutPitch = 2 * 128 + 16;  // LDS staging row: 128 bf16 + 16 bytes
+constexpr int kLmXcds = 8;
+constexpr int kMergeRowsPerBlock = 4;   // rows per 256-thread merge workgroup
+
+static_assert(kLmStages * 2 * kHalfTile <= 4 * 128 * kOutPitch, "staging covers the ring");
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p));
+}
+
+// 16-byte HBM -> LDS copy of every lane: lane i's bytes at gbase + voff land
+// at LDS byte lds + 16*i.  Inline assembly, so that the compiler neither
+// models it nor inserts waits for it; the kernel waits explicitly (s_waitcnt
+// vmcnt) before the barrier that publishes a stage.  m0 is written here;
+// nothing else in the kernel reads m0.
+__device__ __forceinline__ void dma16(const void* gbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(lds), "v"(voff), "s"(gbase)
+               : "memory");
+}
+
+// s_waitcnt immediate: vmcnt <= n, the other counters unconstrained.
+constexpr int vmcnt_encoding(int n) {
+  return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8);
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// max / sum of a value with the same lane of the other 32-lane half (the
+// same bits in both lanes: both operations are symmetric).
+__device__ __forceinline__ float half_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                  false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                  false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Workgroup b -> (vocabulary tile, row tile): the dispatcher places b on XCD
+// b % 8, and the row tiles of one vocabulary tile take consecutive slots of
+// one XCD.
+__device__ __forceinline__ bool tile_of(int b, int v_tiles, int r_tiles, int& vt, int& rt) {
+  const int xcd = b % kLmXcds;
+  const int slot = b / kLmXcds;
+  rt = slot % r_tiles;
+  vt = (slot / r_tiles) * kLmXcds + xcd;
+  return vt < v_tiles;
+}
+
+__global__ __launch_bounds__(kLmThreads, 1) void lm_head_kernel(SgLmHeadArgs a, int v_tiles,
+                                                                 int r_tiles) {
+  __shared__ __align__(1024) unsigned char smem[4 * 128 * kOutPitch];
+  int vt, rt;
+  if (!tile_of(blockIdx.x, v_tiles, r_tiles, vt, rt)) return;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5;
+  const int col = lane & 31;
+  const int V = a.vocab;
+  const int v0 = vt * kTileV;
+  const int r0 = rt * kTileR;
+
+  // DMA slots: per stage each operand is 16 instructions of 1 KiB; wave w
+  // issues instructions 4w .. 4w+3 of both.  Instruction q covers 16-dim block
+  // q >> 3 and tile rows 32*(q & 7) .. +31; lane i moves row 32*(q&7) + i/2,
+  // dims 8*(i&1) .. +7 of that block.  LDS layout of an operand stage:
+  // [16-dim block][256 rows][16 dims], so the MFMA reads below are 1 KiB
+  // contiguous per instruction (no bank conflicts).
+  uint32_t w_off[4], x_off[4], lds_off[4];
+  const unsigned char* wbase =
+      static_cast<const unsigned char*>(a.weight_dev) + static_cast<int64_t>(v0) * a.weight_row_stride * 2;
+  const unsigned char* xbase = static_cast<const unsigned char*>(a.hidden_dev);
+  bool bad_index = false;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int q = wave * 4 + i;
+    const int kb = q >> 3;
+    const int row = 32 * (q & 7) + (lane >> 1);
+    const int dim = 16 * kb + 8 * (lane & 1);
+    // Tokens past the vocabulary re-read the last token (finite data the
+    // epilogue drops); rows past the projected rows re-read a valid row.
+    const int tok = min(v0 + row, V - 1) - v0;
+    w_off[i] = static_cast<uint32_t>((static_cast<int64_t>(tok) * a.weight_row_stride + dim) * 2);
+    const int prow = min(r0 + row, a.num_rows - 1);
+    int src = a.row_index_dev != nullptr ? a.row_index_dev[prow] : prow;
+    if (src < 0 || src >= a.num_hidden_rows) {
+      bad_index = bad_index || (r0 + row < a.num_rows);
+      src = 0;
+    }
+    x_off[i] = static_cast<uint32_t>((static_cast<int64_t>(src) * a.hidden_row_stride + dim) * 2);
+    lds_off[i] = static_cast<uint32_t>(kb * kKbBytes + 1024 * (q & 7));
+  }
+  if (bad_index && a.status_dev != nullptr) atomicExch(a.status_dev, SG_EINVAL);
+
+  const uint32_t ring = lds_addr(smem);
+  const int steps = a.hidden_size / kStepK;
+  auto issue = [&](int s) {
+    const uint32_t stage = ring + (s % kLmStages) * 2 * kHalfTile;
+    const unsigned char* wk = wbase + static_cast<int64_t>(s) * kStepK * 2;
+    const unsigned char* xk = xbase + static_cast<int64_t>(s) * kStepK * 2;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma16(wk, w_off[i], stage + lds_off[i]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma16(xk, x_off[i], stage + kHalfTile + lds_off[i]);
+  };
+
+  floatx16 acc[4][4];
+#pragma unroll
+  for (int vb = 0; vb < 4; ++vb)
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[vb][rb][r] = 0.0f;
+
+  const int wv = wave & 1;   // vocabulary half of the tile
+  const int wr = wave >> 1;  // row half of the tile
+  const int a_lane = (wv * 128 + col) * 32 + 16 * half;
+  const int b_lane = (wr * 128 + col) * 32 + 16 * half;
+
+  // Operand fragments of one stage: weight rows (A) and hidden rows (B) of
+  // both 16-dim blocks, read from LDS one stage ahead of their MFMAs.
+  struct Frags {
+    bf16x8 w[2][4];
+    bf16x8 x[2][4];
+  };
+  auto load_frags = [&](int s, Frags& f) {
+    const unsigned char* st = smem + (s % kLmStages) * 2 * kHalfTile;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int vb = 0; vb < 4; ++vb)
+        f.w[kb][vb] =
+            as_bf16x8(*reinterpret_cast<const uint4*>(st + kb * kKbBytes + a_lane + vb * 1024));
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb)
+        f.x[kb][rb] = as_bf16x8(
+            *reinterpret_cast<const uint4*>(st + kHalfTile + kb * kKbBytes + b_lane + rb * 1024));
+    }
+  };
+  auto mma = [&](const Frags& f) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int vb = 0; vb < 4; ++vb)
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+          acc[vb][rb] =
+              __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.w[kb][vb], f.x[kb][rb], acc[vb][rb], 0, 0, 0);
+  };
+  // Stage s: wait for its copies (only the up to two later stages' remain in
+  // flight), publish it with the barrier (which also ends every wave's reads
+  // of stage s-1), refill stage s-1's slot with stage s+3.
+  auto open_stage = [&](int s) {
+    const int newer = min(kLmStages - 2, steps - 1 - s);
+    if (newer >= 2) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_encoding(16));
+    } else if (newer == 1) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_encoding(8));
+    } else {
+      __builtin_amdgcn_s_waitcnt(vmcnt_encoding(0));
+    }
+    __syncthreads();
+    if (s + kLmStages - 1 < steps) issue(s + kLmStages - 1);
+  };
+
+  for (int s = 0; s < kLmStages - 1 && s < steps; ++s) issue(s);
+  // Software pipeline: the fragments of stage s are read while the MFMAs of
+  // stage s-1 run.
+  // steps is even (hidden_size % 64 == 0): stage 0, pairs of stages, and a
+  // final stage, with no data-dependent branch around the accumulators.
+  Frags f0, f1;
+  open_stage(0);
+  load_frags(0, f0);
+  for (int s = 1; s + 1 < steps; s += 2) {
+    open_stage(s);
+    load_frags(s, f1);
+    mma(f0);
+    open_stage(s + 1);
+    load_frags(s + 1, f0);
+    mma(f1);
+  }
+  open_stage(steps - 1);
+  load_frags(steps - 1, f1);
+  mma(f0);
+  mma(f1);
+  __syncthreads();  // the ring is free: it becomes the output staging area
+
+  // Epilogue.  acc[vb][rb][r] holds token v0 + 128*wv + 32*vb + 8*(r/4) +
+  // 4*half + r%4 of tile row 128*wr + 32*rb + col.
+  const int tok0 = v0 + 128 * wv;           // first token of this wave's statistics tile
+  const bool tile_live = tok0 < V;
+  const int n_tiles = (V + kStatTokens - 1) / kStatTokens;
+  unsigned char* stage = smem + wave * 128 * kOutPitch;
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) {
+    const int row_local = 32 * rb + col;       // row inside this wave's 128 rows
+    const int row = r0 + 128 * wr + row_local;  // projected row
+    float x[64];
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int vb = 0; vb < 4; ++vb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int tok = tok0 + 32 * vb + 8 * (r >> 2) + 4 * half + (r & 3);
+        x[16 * vb + r] = bf16_to_f32(f32_to_bf16(acc[vb][rb][r]));
+        m = (tok < V) ? fmaxf(m, x[16 * vb + r]) : m;
+      }
+    m = half_max(m);
+    // Tokens at or past V add exactly 0 (z stays a non-negative sum).
+    const float mc = (m == -__builtin_inff()) ? 0.0f : m;
+    float z = 0.0f;
+#pragma unroll
+    for (int vb = 0; vb < 4; ++vb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int tok = tok0 + 32 * vb + 8 * (r >> 2) + 4 * half + (r & 3);
+        const float e = sg_exp_nonpos(x[16 * vb + r] - mc);
+        z = z + ((tok < V) ? e : 0.0f);
+      }
+    z = half_sum(z);  // z_0 + z_1
+    if (half == 0 && tile_live && row < a.num_rows) {
+      float* dst = a.tile_stats_dev + (static_cast<int64_t>(row) * n_tiles + tok0 / kStatTokens) * 2;
+      *reinterpret_cast<float2*>(dst) = make_float2(m, z);
+    }
+    // bf16 logits into this wave's staging rows (LDS rows of 128 tokens).
+#pragma unroll
+    for (int vb = 0; vb < 4; ++vb)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint2 packed;
+        packed.x = pack_bf16x2(x[16 * vb + 4 * q], x[16 * vb + 4 * q + 1]);
+        packed.y = pack_bf16x2(x[16 * vb + 4 * q + 2], x[16 * vb + 4 * q + 3]);
+        *reinterpret_cast<uint2*>(stage + row_local * kOutPitch +
+                                  2 * (32 * vb + 8 * q + 4 * half)) = packed;
+      }
+    __builtin_amdgcn_sched_barrier(0);  // one 32-row block at a time (registers)
+  }
+  __builtin_amdgcn_wave_barrier();
+  // Row-contiguous read-back: every instruction moves four 256-byte row
+  // segments (16 lanes x 16 bytes each).
+  if (!tile_live) return;
+  uint16_t* out = static_cast<uint16_t*>(a.logits_dev);
+#pragma unroll 4
+  for (int i = 0; i < 32; ++i) {
+    const int row_local = 4 * i + (lane >> 4);
+    const int row = r0 + 128 * wr + row_local;
+    const int chunk = lane & 15;
+    const int tok = tok0 + 8 * chunk;
+    const uint4 v = *reinterpret_cast<const uint4*>(stage + row_local * kOutPitch + 16 * chunk);
+    if (row >= a.num_rows || tok >= V) continue;
+    uint16_t* dst = out + static_cast<int64_t>(row) * a.logits_row_stride + tok;
+    if (tok + 8 <= V) {
+      *reinterpret_cast<uint4*>(dst) = v;
+    } else {
+      for (int e = 0; tok + e < V; ++e) {
+        const uint32_t w = (e >> 1) == 0 ? v.x : (e >> 1) == 1 ? v.y : (e >> 1) == 2 ? v.z : v.w;
+        dst[e] = static_cast<uint16_t>((e & 1) ? (w >> 16) : (w & 0xffffu));
+      }
+    }
+  }
+}
+
+// Row (max, sum) from the tile pairs: one wave per row; lane l merges tiles
+// l, l+64, ... in increasing order, then the xor butterfly merges the lanes.
+__global__ __launch_bounds__(kMergeRowsPerBlock * kWave) void lm_head_rows_kernel(SgLmHeadArgs a) {
+  const int row = blockIdx.x * kMergeRowsPerBlock + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= a.num_rows) return;
+  const int n_tiles = (a.vocab + kStatTokens - 1) / kStatTokens;
+  const float2* tiles =
+      reinterpret_cast<const float2*>(a.tile_stats_dev) + static_cast<int64_t>(row) * n_tiles;
+  MZ acc = {-__builtin_inff(), 0.0f};
+  for (int t = lane; t < n_tiles; t += kWave) {
+    const float2 p = tiles[t];
+    acc = merge_mz(acc, MZ{p.x, p.y});
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    const MZ other = {__shfl_xor(acc.m, d), __shfl_xor(acc.z, d)};
+    acc = merge_mz(acc, other);
+  }
+  if (lane == 0) {
+    a.row_max_dev[row] = acc.m;
+    a.row_sum_dev[row] = acc.z;
+  }
+}
+
+}  // namespace
+}  // namespace sg
+
+extern "C" int64_t sg_lm_head_tile_count(int32_t vocab) {
+  return vocab >= 1 ? (static_cast<int64_t>(vocab) + sg::kStatTokens - 1) / sg::kStatTokens : -1;
+}
+
+extern "C" int sg_lm_head(const SgLmHeadArgs* args, sg_stream_t stream) {
+  using namespace sg;
+  clear_error();
+  SG_REQUIRE(args != nullptr, "null args");
+  const SgLmHeadArgs& a = *args;
+  SG_REQUIRE(a.num_rows >= 0, "num_rows must be non-negative");
+  SG_REQUIRE(a.vocab >= 1, "vocab must be positive");
+  SG_REQUIRE(a.hidden_size >= 2 * kStepK && a.hidden_size % (2 * kStepK) == 0,
+             "hidden_size must be a positive multiple of 64");
+  if (a.num_rows == 0) return SG_OK;
+  SG_REQUIRE(a.num_hidden_rows >= 1, "num_hidden_rows must be positive");
+  SG_REQUIRE(a.row_index_dev != nullptr || a.num_hidden_rows >= a.num_rows,
+             "without a row index the hidden rows must cover every projected row");
+  SG_REQUIRE(a.hidden_dev && a.weight_dev && a.logits_dev && a.tile_stats_dev &&
+                 a.row_max_dev && a.row_sum_dev,
+             "null device pointer");
+  SG_REQUIRE(a.hidden_row_stride >= a.hidden_size && a.weight_row_stride >= a.hidden_size &&
+                 a.logits_row_stride >= a.vocab,
+             "row strides must cover the rows");
+  SG_REQUIRE((a.hidden_row_stride | a.weight_row_stride | a.logits_row_stride) % 8 == 0,
+             "row strides must be multiples of 8 elements");
+  SG_REQUIRE((reinterpret_cast<uintptr_t>(a.hidden_dev) | reinterpret_cast<uintptr_t>(a.weight_dev) |
+              reinterpret_cast<uintptr_t>(a.logits_dev)) % 16 == 0,
+             "hidden, weight and logits must be 16-byte aligned");
+  // The per-lane copy offsets are 32-bit: a tile's weight rows and the whole
+  // hidden matrix must each stay below 4 GiB.
+  SG_REQUIRE(static_cast<int64_t>(kTileV) * a.weight_row_stride * 2 < (int64_t{1} << 32),
+             "weight rows too long");
+  SG_REQUIRE(static_cast<int64_t>(a.num_hidden_rows) * a.hidden_row_stride * 2 < (int64_t{1} << 32),
+             "hidden matrix above 4 GiB");
+  const int v_tiles = (a.vocab + kTileV - 1) / kTileV;
+  const int r_tiles = (a.num_rows + kTileR - 1) / kTileR;
+  const int64_t blocks =
+      static_cast<int64_t>((v_tiles + kLmXcds - 1) / kLmXcds) * kLmXcds * r_tiles;
+  SG_REQUIRE(blocks < INT32_MAX, "wave too large");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  lm_head_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kLmThreads), 0, s>>>(a, v_tiles,
+                                                                                  r_tiles);
+  SG_LAUNCH_CHECK();
+  const int merge_blocks = (a.num_rows + kMergeRowsPerBlock - 1) / kMergeRowsPerBlock;
+  lm_head_rows_kernel<<<dim3(merge_blocks), dim3(kMergeRowsPerBlock * kWave), 0, s>>>(a);
+  SG_LAUNCH_CHECK();
+  return SG_OK;
+}

@@ -31,6 +31,7 @@
 #include <type_traits>
 
 #include "sg_common.h"
+#include "sg_math.h"
 
 namespace sg {
 namespace {
@@ -45,74 +46,9 @@ constexpr int kWalkWaves = kWalkThreads / kWave;
 constexpr int kMaxTreeRows = 1024;
 // Per-request record that the walk's part 1 leaves for part 2 in the
 // workspace, after the slab and line totals: accept length (-1 for a broken
-// walk), exit node, child count, pad, then the exit node's child tokens.
+// walk), exit node, child count, exit logits row (-1: an unprojected leaf), then
+// the exit node's child tokens.
 constexpr int kRecordInts = 4 + kMaxTreeRows;
-
-#define SG_LOG2E 0x1.715476p+0f
-#define SG_LN2_HI 0x1.62e4p-1f
-#define SG_LN2_LO 0x1.7f7d1cp-20f
-#define SG_C6 0x1.6c16c2p-10f
-#define SG_C5 0x1.111112p-7f
-#define SG_C4 0x1.555556p-5f
-#define SG_C3 0x1.555556p-3f
-
-// E(x): 0 below -87 (and for NaN), Cody-Waite reduction with a split ln2,
-// degree-6 Taylor polynomial in Horner form, exact scale by 2^n.
-__device__ __forceinline__ float sg_exp(float x) {
-  const bool live = x >= -87.0f;
-  const float xc = fminf(fmaxf(x, -87.0f), 88.0f);
-  const float n = __builtin_rintf(xc * SG_LOG2E);
-  float r = __builtin_fmaf(-n, SG_LN2_HI, xc);
-  r = __builtin_fmaf(-n, SG_LN2_LO, r);
-  float p = SG_C6;
-  p = __builtin_fmaf(p, r, SG_C5);
-  p = __builtin_fmaf(p, r, SG_C4);
-  p = __builtin_fmaf(p, r, SG_C3);
-  p = __builtin_fmaf(p, r, 0.5f);
-  p = __builtin_fmaf(p, r, 1.0f);
-  p = __builtin_fmaf(p, r, 1.0f);
-  // p * 2^n, exact scale (n in [-126, 127]); ldexp rounds a subnormal result
-  // exactly as the multiplication by the normal power of two would.
-  float y = __builtin_ldexpf(p, static_cast<int>(n));
-  y = (x > 88.0f) ? __builtin_inff() : y;
-  return live ? y : 0.0f;
-}
-
-// E(x) for x <= 0 (every argument of the form value - max): the same
-// operations as sg_exp without the upper clamp and overflow select, which
-// cannot apply there, and without the lower clamp: it leaves every live x
-// (x >= -87) unchanged, and the final select returns 0 for the others
-// whatever the polynomial gave them.  The results are identical.
-__device__ __forceinline__ float sg_exp_nonpos(float x) {
-  const bool live = x >= -87.0f;
-  const float xc = x;
-  const float n = __builtin_rintf(xc * SG_LOG2E);
-  float r = __builtin_fmaf(-n, SG_LN2_HI, xc);
-  r = __builtin_fmaf(-n, SG_LN2_LO, r);
-  float p = SG_C6;
-  p = __builtin_fmaf(p, r, SG_C5);
-  p = __builtin_fmaf(p, r, SG_C4);
-  p = __builtin_fmaf(p, r, SG_C3);
-  p = __builtin_fmaf(p, r, 0.5f);
-  p = __builtin_fmaf(p, r, 1.0f);
-  p = __builtin_fmaf(p, r, 1.0f);
-  const float y = __builtin_ldexpf(p, static_cast<int>(n));
-  return live ? y : 0.0f;
-}
-
-struct MZ {
-  float m;
-  float z;
-};
-
-__device__ __forceinline__ MZ merge_mz(MZ a, MZ b) {
-  MZ out;
-  out.m = fmaxf(a.m, b.m);
-  const float left = a.z * sg_exp(a.m - out.m);
-  const float right = b.z * sg_exp(b.m - out.m);
-  out.z = (out.m == -__builtin_inff()) ? 0.0f : left + right;
-  return out;
-}
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -341,10 +277,12 @@ struct RouteShared {
   float rz[kMaxTreeRows];
   float u[2 * kMaxTreeRows + 2];
   int child_tok[kMaxTreeRows];  // children of the exit node, ascending node order
+  int lrow[kMaxTreeRows];       // logits row of each node, -1 when not projected
   int child_count;
   int exit_node;
   int depth;
   int broken;
+  int bad_rows;  // a node with children has no logits row, or a row is out of range
 };
 
 // Gathers everything the routing reads in one parallel round (the tree, the
@@ -360,17 +298,33 @@ __device__ void route_request(const SgTreeSampleArgs& a, int req, int r0, int n,
   const int tid = threadIdx.x;
   const float* __restrict__ u = a.uniforms_dev + static_cast<int64_t>(a.uniform_stride) * req;
   const int n_u = min(a.uniform_stride, 2 * kMaxTreeRows + 2);
+  const int n_logits = a.num_logits_rows > 0 ? a.num_logits_rows : a.num_rows;
+  // Round 1: the tree, each node's logits row and the uniforms.
+  if (tid == 0) sh.bad_rows = 0;
   for (int k = tid; k < n; k += blockDim.x) {
-    const int p = a.parent_dev[r0 + k];
-    const int tok = a.token_dev[r0 + k];
-    sh.parent[k] = p;
-    sh.token[k] = tok;
-    sh.rm[k] = a.row_max_dev[r0 + k];
-    sh.rz[k] = a.row_sum_dev[r0 + k];
-    const bool readable = k > 0 && p >= 0 && p < k && tok >= 0 && tok < a.vocab;
-    sh.xchild[k] = readable ? to_f32(logits[a.logits_row_stride * (r0 + p) + tok]) : 0.0f;
+    sh.parent[k] = a.parent_dev[r0 + k];
+    sh.token[k] = a.token_dev[r0 + k];
+    sh.lrow[k] = a.logits_row_dev != nullptr ? a.logits_row_dev[r0 + k] : r0 + k;
   }
   for (int k = tid; k < n_u; k += blockDim.x) sh.u[k] = u[k];
+  __syncthreads();
+  // Round 2: the row statistics and each node's token logit in its parent's
+  // row (the only logits routing touches).  A node whose parent has no
+  // logits row breaks the lazy-projection contract.
+  for (int k = tid; k < n; k += blockDim.x) {
+    const int lr = sh.lrow[k];
+    const bool own = lr >= 0 && lr < n_logits;
+    sh.rm[k] = own ? a.row_max_dev[lr] : -__builtin_inff();
+    sh.rz[k] = own ? a.row_sum_dev[lr] : 0.0f;
+    const int p = sh.parent[k];
+    const int tok = sh.token[k];
+    const bool edge = k > 0 && p >= 0 && p < k;
+    const int pr = edge ? sh.lrow[p] : -1;
+    const bool prow_ok = pr >= 0 && pr < n_logits;
+    const bool readable = edge && prow_ok && tok >= 0 && tok < a.vocab;
+    sh.xchild[k] = readable ? to_f32(logits[a.logits_row_stride * pr + tok]) : 0.0f;
+    if (lr >= n_logits || (edge && !prow_ok)) sh.bad_rows = 1;
+  }
   __syncthreads();
   // Wave 0 walks; every lane holds the same state.  The children of v, in
   // ascending node order, are the nodes c > v with parent v, found 64 at a
@@ -380,8 +334,9 @@ __device__ void route_request(const SgTreeSampleArgs& a, int req, int r0, int n,
     int32_t* nodes_out = a.accept_nodes_dev + static_cast<int64_t>(a.max_depth) * req;
     int v = 0;
     int depth = 0;
-    int broken = 0;
+    int broken = sh.bad_rows;
     for (;;) {
+      if (broken) break;
       if (2 * depth + 1 >= a.uniform_stride || 2 * depth + 1 >= n_u) {
         broken = 1;
         break;
@@ -459,6 +414,7 @@ __global__ __launch_bounds__(kWalkThreads) void exit_totals_kernel(SgTreeSampleA
     if (chunk == 0 && tid == 0) {
       a.accept_len_dev[req] = -1;
       a.bonus_dev[req] = -1;
+      if (a.terminal_leaf_dev) a.terminal_leaf_dev[req] = -1;
       if (a.status_dev) atomicExch(a.status_dev, SG_EINVAL);
     }
     return;
@@ -468,9 +424,14 @@ __global__ __launch_bounds__(kWalkThreads) void exit_totals_kernel(SgTreeSampleA
     for (int k = tid; k < a.max_depth; k += blockDim.x) nodes_out[k] = -1;
   __syncthreads();
   route_request<S>(a, req, r0, n, sh, chunk == 0);
+  // The walk ended at a node whose row was not projected (a leaf): no exit
+  // draw here; the caller projects that leaf and draws its bonus.
+  const int exit_row = sh.broken ? -1 : sh.lrow[sh.exit_node];
   if (chunk == 0) {
     if (tid == 0) {
       a.accept_len_dev[req] = sh.broken ? -1 : sh.depth;
+      if (a.terminal_leaf_dev)
+        a.terminal_leaf_dev[req] = (!sh.broken && exit_row < 0) ? sh.exit_node : -1;
       if (sh.broken) {
         a.bonus_dev[req] = -1;
         if (a.status_dev) atomicExch(a.status_dev, SG_EINVAL);
@@ -491,16 +452,15 @@ __global__ __launch_bounds__(kWalkThreads) void exit_totals_kernel(SgTreeSampleA
       rec[0] = sh.broken ? -1 : sh.depth;
       rec[1] = sh.exit_node;
       rec[2] = sh.child_count;
-      rec[3] = 0;
+      rec[3] = exit_row;
     }
     for (int k = tid; k < sh.child_count; k += blockDim.x) rec[4 + k] = sh.child_tok[k];
   }
-  if (sh.broken) return;
+  if (sh.broken || exit_row < 0) return;
   const int slabs = (a.vocab + kSlab - 1) / kSlab;
   const int s = chunk * kWalkWaves + wave;
   if (s >= slabs) return;
-  const int64_t row = r0 + sh.exit_node;
-  const S* __restrict__ x = static_cast<const S*>(a.logits_dev) + a.logits_row_stride * row;
+  const S* __restrict__ x = static_cast<const S*>(a.logits_dev) + a.logits_row_stride * exit_row;
   const float m = sh.rm[sh.exit_node];
   float e[32], incl[kLinesPerSlab], total[kLinesPerSlab];
   exit_values<S, kVec>(x, a.vocab, m, s, lane, child_bits(sh.child_tok, sh.child_count, s, lane),
@@ -545,12 +505,11 @@ __global__ __launch_bounds__(kWave) void exit_find_kernel(SgTreeSampleArgs a) {
                            static_cast<int64_t>(a.num_requests) * slabs * (1 + kLinesPerSlab)) +
                        static_cast<int64_t>(req) * kRecordInts;
   const float* __restrict__ u = a.uniforms_dev + static_cast<int64_t>(a.uniform_stride) * req;
-  // One round trip: the row range, part 1's record (accept length, exit node,
-  // child count), the first 64 child tokens and the slab totals.
+  // One round trip: the row range, part 1's record (accept length, child
+  // count, exit row), the first 64 child tokens and the slab totals.
   const int r0 = a.row_offset_dev[req];
   const int n = a.row_offset_dev[req + 1] - r0;
   const int depth = rec[0];
-  const int v = rec[1];
   const int count = rec[2];
   const int tok0 = rec[4 + lane];
   float tot[(kMaxSlabs + kWave - 1) / kWave];
@@ -560,6 +519,11 @@ __global__ __launch_bounds__(kWave) void exit_find_kernel(SgTreeSampleArgs a) {
   // The record exists only for a valid tree; part 1 reported the others.
   if (n < 1 || n > kMaxTreeRows || r0 < 0 || r0 > a.num_rows - n) return;
   if (depth < 0) return;  // broken walk, reported by part 1
+  const int exit_row = rec[3];
+  if (exit_row < 0) {      // terminal leaf without a projected row
+    if (lane == 0) a.bonus_dev[req] = -1;
+    return;
+  }
   if (lane < count) s_child_tok[lane] = tok0;
   for (int k = kWave + lane; k < count; k += kWave) s_child_tok[k] = rec[4 + k];
 #pragma unroll
@@ -568,7 +532,7 @@ __global__ __launch_bounds__(kWave) void exit_find_kernel(SgTreeSampleArgs a) {
   // The exit draw's uniform and the exit row's max, in flight during the
   // sums below.
   const float u_exit = u[2 * depth + 1];
-  const int64_t row = static_cast<int64_t>(r0) + v;
+  const int64_t row = exit_row;
   const float m = a.row_max_dev[row];
   __builtin_amdgcn_wave_barrier();
   // C and the threshold (every lane runs the same sequential sums).
@@ -767,6 +731,13 @@ int check_sample_args(const SgTreeSampleArgs* args) {
   SG_REQUIRE(a.max_depth >= 0, "max_depth must be non-negative");
   SG_REQUIRE(a.uniform_stride >= 2 * (a.max_depth + 1),
              "uniform_stride must cover 2*(max_depth+1) uniforms");
+  SG_REQUIRE((a.flags & ~SG_SAMPLE_STATS_READY) == 0, "unknown sampler flags");
+  SG_REQUIRE(a.num_logits_rows >= 0, "negative num_logits_rows");
+  SG_REQUIRE(a.logits_row_dev != nullptr || a.num_logits_rows == 0 ||
+                 a.num_logits_rows == a.num_rows,
+             "without a logits row map the logits rows are the packed rows");
+  SG_REQUIRE(a.logits_row_dev == nullptr || a.terminal_leaf_dev != nullptr,
+             "a logits row map needs terminal_leaf_dev for walks that end at an unprojected leaf");
   if (a.num_requests == 0) return SG_OK;
   SG_REQUIRE(a.logits_dev && a.row_offset_dev && a.parent_dev && a.token_dev &&
                  a.uniforms_dev && a.row_max_dev && a.row_sum_dev && a.accept_len_dev &&
@@ -778,8 +749,11 @@ int check_sample_args(const SgTreeSampleArgs* args) {
 // Enqueues the three kernels of one sampling call; a.workspace_dev holds at
 // least sg_tree_sample_workspace_bytes(num_requests, vocab) bytes.
 int launch_tree_sample(const SgTreeSampleArgs& a, hipStream_t s) {
+  // With SG_SAMPLE_STATS_READY the statistics pass only clears the status.
+  const int stats_rows = (a.flags & SG_SAMPLE_STATS_READY) ? 0
+                         : (a.num_logits_rows > 0 ? a.num_logits_rows : a.num_rows);
   int rc = launch_row_stats(a.logits_dev, a.logits_dtype, a.logits_row_stride, a.vocab,
-                            a.num_rows, a.row_max_dev, a.row_sum_dev, a.status_dev, s);
+                            stats_rows, a.row_max_dev, a.row_sum_dev, a.status_dev, s);
   if (rc != SG_OK) return rc;
   const int slabs = (a.vocab + kSlab - 1) / kSlab;
   const dim3 grid1(a.num_requests, (slabs + kWalkWaves - 1) / kWalkWaves);

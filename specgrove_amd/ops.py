@@ -435,8 +435,9 @@ def _sample_args(logits, row_offset, parent, token, uniforms, max_depth, out, n,
     a.token_dev = token.data_ptr()
     a.uniforms_dev = uniforms.data_ptr()
     a.uniform_stride = uniforms.shape[1]
-    a.row_max_dev = out.row_max.data_ptr()
-    a.row_sum_dev = out.row_sum.data_ptr()
+    a.row_max_dev = out.row_max.data_ptr() if hasattr(out, "row_max") else 0
+    a.row_sum_dev = out.row_sum.data_ptr() if hasattr(out, "row_sum") else 0
+    a.num_logits_rows = logits.shape[0]
     a.accept_nodes_dev = out.accept_nodes.data_ptr()
     a.accept_len_dev = out.accept_len.data_ptr()
     a.bonus_dev = out.bonus.data_ptr()
@@ -497,6 +498,73 @@ def tree_sample_noalloc(logits: torch.Tensor, row_offset: torch.Tensor, parent: 
     return out
 
 
+@dataclass
+class ProjectedSampleResult:
+    accept_nodes: torch.Tensor   # [n, max_depth] i32, -1 padded
+    accept_len: torch.Tensor     # [n] i32
+    bonus: torch.Tensor          # [n] i32, -1 where the walk ended at an unprojected leaf
+    keep_rows: torch.Tensor      # [n, max_depth + 1] i32
+    terminal_leaf: torch.Tensor  # [n] i32: that leaf's local node id, else -1
+    status: torch.Tensor         # [1] i32
+    workspace: torch.Tensor
+
+
+def tree_sample_projected(logits: torch.Tensor, row_offset: torch.Tensor, parent: torch.Tensor,
+                          token: torch.Tensor, uniforms: torch.Tensor, max_depth: int, *,
+                          row_max: torch.Tensor, row_sum: torch.Tensor,
+                          row_map: torch.Tensor | None = None) -> ProjectedSampleResult:
+    """The tree walk over LM-head logits whose statistics are already known
+    (``lm_head`` wrote them): sg_tree_sample with SG_SAMPLE_STATS_READY.
+
+    ``logits`` [Rp, V] holds the projected rows; ``row_map`` [R] i32 gives
+    each packed node's logits row, -1 for a node that was not projected (only
+    nodes without children; a walk that ends there reports it in
+    ``terminal_leaf`` and leaves its bonus -1), None when row r is node r.
+    ``row_max``/``row_sum`` [Rp] f32 are the LM head's row statistics.
+    """
+    _check_logits(logits)
+    for t, name in ((row_offset, "row_offset"), (parent, "parent"), (token, "token")):
+        _check_device_tensor(t, name, torch.int32)
+        _require(t.is_contiguous(), f"{name} must be contiguous")
+    _check_device_tensor(uniforms, "uniforms", torch.float32)
+    _require(uniforms.dim() == 2 and uniforms.is_contiguous(), "uniforms must be [n, U]")
+    n = row_offset.numel() - 1
+    rows = parent.numel()
+    logit_rows = logits.shape[0]
+    _require(uniforms.shape[0] == n, "one uniform row per request")
+    _require(uniforms.shape[1] >= 2 * (max_depth + 1), "uniforms must cover 2*(max_depth+1)")
+    _require(token.numel() == rows, "parent and token must both cover the R packed rows")
+    for t, name in ((row_max, "row_max"), (row_sum, "row_sum")):
+        _check_device_tensor(t, name, torch.float32)
+        _require(t.numel() == logit_rows and t.is_contiguous(), f"{name} must be [Rp]")
+    if row_map is None:
+        _require(logit_rows == rows, "without a row map the logits rows are the packed rows")
+    else:
+        _check_device_tensor(row_map, "row_map", torch.int32)
+        _require(row_map.numel() == rows and row_map.is_contiguous(), "row_map must be [R]")
+    dev = logits.device
+    depth_slots = max(max_depth, 1)
+    ws_bytes = int(_lib.load().sg_tree_sample_workspace_bytes(n, logits.shape[1]))
+    out = ProjectedSampleResult(
+        accept_nodes=torch.empty((n, depth_slots), dtype=torch.int32, device=dev),
+        accept_len=torch.empty(n, dtype=torch.int32, device=dev),
+        bonus=torch.empty(n, dtype=torch.int32, device=dev),
+        keep_rows=torch.empty((n, max_depth + 1), dtype=torch.int32, device=dev),
+        terminal_leaf=torch.empty(n, dtype=torch.int32, device=dev),
+        status=torch.zeros(1, dtype=torch.int32, device=dev),
+        workspace=torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev))
+    a = _sample_args(logits, row_offset, parent, token, uniforms, max_depth, out, n, rows,
+                     out.workspace)
+    a.row_max_dev = row_max.data_ptr()
+    a.row_sum_dev = row_sum.data_ptr()
+    a.logits_row_dev = row_map.data_ptr() if row_map is not None else 0
+    a.num_logits_rows = logit_rows
+    a.flags = _lib.SG_SAMPLE_STATS_READY
+    a.terminal_leaf_dev = out.terminal_leaf.data_ptr()
+    _lib.check(_lib.load().sg_tree_sample(ctypes.byref(a), _stream_handle()), "sg_tree_sample")
+    return out
+
+
 def row_stats(logits: torch.Tensor):
     dtype = _check_logits(logits)
     rows = logits.shape[0]
@@ -516,3 +584,66 @@ def exp_probe(x: torch.Tensor) -> torch.Tensor:
     _lib.check(_lib.load().sg_exp_probe(x.data_ptr(), out.data_ptr(), x.numel(),
                                         _stream_handle()), "sg_exp_probe")
     return out
+
+
+# --------------------------------------------------------------------------
+# (D) LM head with fused statistics
+# --------------------------------------------------------------------------
+
+@dataclass
+class LmHeadResult:
+    logits: torch.Tensor      # [Rp, V] bf16 (a view of rows padded to 8 elements)
+    tile_stats: torch.Tensor  # [Rp, ceil(V/128), 2] f32: (max, sum of E(x - max)) per tile
+    row_max: torch.Tensor     # [Rp] f32
+    row_sum: torch.Tensor     # [Rp] f32
+    status: torch.Tensor      # [1] i32: SG_EINVAL when a row index was out of range
+
+
+def lm_head(hidden: torch.Tensor, weight: torch.Tensor,
+            row_index: torch.Tensor | None = None) -> LmHeadResult:
+    """bf16 logits of the selected hidden rows and their softmax statistics
+    (sg_lm_head).
+
+    ``hidden`` [N, H] bf16 (row-contiguous, H a multiple of 64), ``weight``
+    [V, H] bf16 (``lm_head.weight``), ``row_index`` [Rp] i32 selects the rows
+    to project (None: all N).  Replaces ``lm_head(hidden)`` +
+    ``probabilities(...)`` on the rows a tree walk can need
+    (fused_tree_sampling.py:2899-2913, :2974-2984).
+    """
+    for t, name in ((hidden, "hidden"), (weight, "weight")):
+        _check_device_tensor(t, name, torch.bfloat16)
+        _require(t.dim() == 2 and t.stride(1) == 1, f"{name} must be a row-contiguous matrix")
+    _require(hidden.shape[1] == weight.shape[1], "hidden and weight disagree on the hidden size")
+    if row_index is not None:
+        _check_device_tensor(row_index, "row_index", torch.int32)
+        _require(row_index.dim() == 1 and row_index.is_contiguous(), "row_index must be [Rp]")
+    rows = row_index.numel() if row_index is not None else hidden.shape[0]
+    vocab, hsize = weight.shape
+    dev = hidden.device
+    pad = (vocab + 7) // 8 * 8
+    tiles = int(_lib.load().sg_lm_head_tile_count(vocab))
+    logits = torch.empty((rows, pad), dtype=torch.bfloat16, device=dev)
+    res = LmHeadResult(
+        logits=logits[:, :vocab],
+        tile_stats=torch.empty((rows, tiles, 2), dtype=torch.float32, device=dev),
+        row_max=torch.empty(rows, dtype=torch.float32, device=dev),
+        row_sum=torch.empty(rows, dtype=torch.float32, device=dev),
+        status=torch.zeros(1, dtype=torch.int32, device=dev))
+    a = _lib.SgLmHeadArgs()
+    a.num_rows = rows
+    a.hidden_size = hsize
+    a.vocab = vocab
+    a.num_hidden_rows = hidden.shape[0]
+    a.hidden_dev = hidden.data_ptr()
+    a.hidden_row_stride = hidden.stride(0)
+    a.row_index_dev = row_index.data_ptr() if row_index is not None else 0
+    a.weight_dev = weight.data_ptr()
+    a.weight_row_stride = weight.stride(0)
+    a.logits_dev = logits.data_ptr()
+    a.logits_row_stride = pad
+    a.tile_stats_dev = res.tile_stats.data_ptr()
+    a.row_max_dev = res.row_max.data_ptr()
+    a.row_sum_dev = res.row_sum.data_ptr()
+    a.status_dev = res.status.data_ptr()
+    _lib.check(_lib.load().sg_lm_head(ctypes.byref(a), _stream_handle()), "sg_lm_head")
+    return res

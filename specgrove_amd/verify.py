@@ -138,3 +138,187 @@ def tree_verify_hip_rejection(parents, tokens, all_logits: torch.Tensor,
     validate) -> (nodes, tokens, bonus)`` (reference sampling.py:903-950)."""
     return tree_verify_hip_rejection_batched([parents], [tokens], all_logits,
                                              generators=[generator], validate=validate)[0]
+
+
+LAZY_VERIFIER_NAME = "hip_lazy_projection"
+
+
+def _head_weight(lm_head) -> torch.Tensor:
+    """The [V, H] bf16 weight of an ``nn.Linear`` vocabulary head (no bias) or
+    the weight tensor itself."""
+    weight = getattr(lm_head, "weight", lm_head)
+    if getattr(lm_head, "bias", None) is not None:
+        raise ValueError("The HIP lazy projection supports a vocabulary head without bias")
+    if (not isinstance(weight, torch.Tensor) or weight.dim() != 2 or not weight.is_cuda
+            or weight.dtype != torch.bfloat16):
+        raise ValueError("The HIP lazy projection needs a bf16 [V, H] head weight on the GPU")
+    return weight if weight.stride(1) == 1 else weight.contiguous()
+
+
+def tree_verify_hip_lazy_projection_batched(parents_batch: Sequence[Sequence[int]],
+                                            tokens_batch: Sequence[Sequence[int]],
+                                            final_hidden: torch.Tensor, lm_head,
+                                            temperature: float = 1.0,
+                                            probability_dtype=torch.float32,
+                                            generators=None, validate: bool = True):
+    """Lazy vocabulary projection with exact sparse-exit routing on the HIP
+    kernels (reference ``tree_verify_ancestral_lazy_projection_sparse_exit_batched``,
+    fused_tree_sampling.py:2840-3031; law sampling.py:738-832).
+
+    All internal rows of the wave (nodes with children) are projected by one
+    ``sg_lm_head`` call, whose epilogue leaves their softmax statistics; the
+    walks route on them, and a walk that reaches a leaf leaves it for a second
+    projection of only the reached leaves, from whose rows the bonus is drawn
+    (``u[2d+1]`` over the whole row).  The output law is that of projecting
+    every row: a leaf row cannot influence which leaf is reached.
+
+    ``final_hidden`` is ``[B, N, H]`` (equal trees, as the reference) or the
+    packed wave ``[R, H]`` / ``[1, R, H]``; ``lm_head`` an ``nn.Linear``
+    without bias (or its bf16 ``[V, H]`` weight).  Returns, per request,
+    ``(nodes, tokens, bonus, stats)`` with the reference's projection counts.
+    """
+    count = len(parents_batch)
+    if (count < 1 or len(tokens_batch) != count or generators is None
+            or len(generators) != count or not isinstance(final_hidden, torch.Tensor)
+            or not final_hidden.is_cuda or final_hidden.dtype != torch.bfloat16):
+        raise ValueError("Batched lazy-projection inputs are inconsistent")
+    if (not isinstance(temperature, (float, int)) or not math.isfinite(float(temperature))
+            or float(temperature) != 1.0):
+        raise ValueError("The HIP lazy projection samples at temperature 1")
+    if probability_dtype != torch.float32:
+        raise ValueError("The HIP lazy projection uses fp32 probability arithmetic")
+    weight = _head_weight(lm_head)
+    topologies = [_topology(p, t) for p, t in zip(parents_batch, tokens_batch)]
+    rows = [len(p) for p, _, _ in topologies]
+    total = sum(rows)
+    hidden_size = final_hidden.shape[-1]
+    if final_hidden.dim() == 3 and final_hidden.shape[0] == count and count > 1:
+        if any(r != final_hidden.shape[1] for r in rows):
+            raise ValueError("Batched lazy-projection hidden shape mismatch")
+        hidden = final_hidden.reshape(count * final_hidden.shape[1], hidden_size)
+    elif final_hidden.dim() == 3 and final_hidden.shape[0] == 1:
+        hidden = final_hidden[0]
+    elif final_hidden.dim() == 2:
+        hidden = final_hidden
+    else:
+        raise ValueError("Batched lazy-projection hidden shape mismatch")
+    if hidden.shape[0] != total or hidden_size != weight.shape[1]:
+        raise ValueError("Batched lazy-projection hidden shape mismatch")
+    if hidden.stride(1) != 1:
+        hidden = hidden.contiguous()
+    vocab = weight.shape[0]
+    if any(token < 0 or token >= vocab for _, tokens, _ in topologies for token in tokens):
+        raise ValueError("Tree token is outside the Target vocabulary")
+
+    device = hidden.device
+    row_offset = np.zeros(count + 1, np.int32)
+    np.cumsum(rows, out=row_offset[1:])
+    # Internal nodes (those with children) in ascending packed order.
+    row_map = np.full(total, -1, np.int32)
+    internal_counts = []
+    for i, (parents, _, _) in enumerate(topologies):
+        internal = sorted(set(parents[1:]))
+        internal_counts.append(len(internal))
+        for node in internal:
+            row_map[row_offset[i] + node] = 0
+    internal_rows = np.flatnonzero(row_map >= 0).astype(np.int32)
+    row_map[internal_rows] = np.arange(internal_rows.size, dtype=np.int32)
+    parent = np.concatenate([np.asarray(p, np.int32) for p, _, _ in topologies])
+    token = np.concatenate([np.asarray([-1] + list(t), np.int32) for _, t, _ in topologies])
+    meta = torch.from_numpy(np.concatenate([row_offset, parent, token, row_map,
+                                            internal_rows])).to(device)
+    n1 = count + 1
+    meta_row_offset = meta[:n1]
+    meta_parent = meta[n1:n1 + total]
+    meta_token = meta[n1 + total:n1 + 2 * total]
+    meta_row_map = meta[n1 + 2 * total:n1 + 3 * total]
+    meta_internal = meta[n1 + 3 * total:]
+
+    max_depth = max(depth for _, _, depth in topologies)
+    stride = 2 * (max_depth + 1)
+    uniforms = torch.zeros((count, stride), dtype=torch.float32, device=device)
+    for i, ((_, _, depth), generator) in enumerate(zip(topologies, generators)):
+        uniforms[i, :2 * (depth + 1)] = torch.rand(2 * (depth + 1), dtype=torch.float32,
+                                                   device=device, generator=generator)
+
+    def projection_valid(head: "ops.LmHeadResult") -> torch.Tensor:
+        ok = (torch.isfinite(head.row_max).all() & torch.isfinite(head.row_sum).all()
+              & (head.row_sum > 0).all() & (head.status == 0).all())
+        return ok.to(torch.int32).reshape(1)
+
+    if internal_rows.size:
+        head = ops.lm_head(hidden, weight, meta_internal)
+        logits, row_max, row_sum = head.logits, head.row_max, head.row_sum
+        valid = projection_valid(head)
+    else:  # no tree has an edge: every walk ends at its (unprojected) root
+        logits = torch.zeros((1, vocab), dtype=torch.bfloat16, device=device)
+        row_max = torch.zeros(1, dtype=torch.float32, device=device)
+        row_sum = torch.ones(1, dtype=torch.float32, device=device)
+        valid = torch.ones(1, dtype=torch.int32, device=device)
+    result = ops.tree_sample_projected(logits, meta_row_offset, meta_parent, meta_token,
+                                       uniforms, max_depth, row_max=row_max, row_sum=row_sum,
+                                       row_map=meta_row_map)
+    # One device-to-host transfer for the walks.
+    width = result.accept_nodes.shape[1]
+    host = torch.cat([result.accept_len, result.bonus, result.terminal_leaf,
+                      result.accept_nodes.reshape(-1), result.status, valid]).tolist()
+    lengths = host[:count]
+    bonuses = host[count:2 * count]
+    leaves = host[2 * count:3 * count]
+    nodes_flat = host[3 * count:3 * count + count * width]
+    if validate and host[-1] != 1:
+        raise FloatingPointError("Invalid batched internal probabilities")
+    if host[-2] != 0:
+        raise RuntimeError("HIP tree sampler returned invalid control values")
+
+    leaf_requests = [i for i in range(count) if leaves[i] >= 0]
+    if leaf_requests:
+        # Second projection: the reached leaves only; each draws its bonus from
+        # the whole row with its exit uniform u[2d+1] (a one-node walk).
+        m = len(leaf_requests)
+        leaf_rows = [int(row_offset[i]) + leaves[i] for i in leaf_requests]
+        exit_cols = [2 * lengths[i] + 1 for i in leaf_requests]
+        leaf_meta = torch.tensor(leaf_rows + list(range(m + 1)) + [-1] * m + [0] * m
+                                 + leaf_requests + exit_cols, dtype=torch.int32)
+        leaf_meta = leaf_meta.to(device)
+        leaf_index = leaf_meta[:m]
+        single_offset = leaf_meta[m:2 * m + 1]
+        single_parent = leaf_meta[2 * m + 1:3 * m + 1]
+        single_token = leaf_meta[3 * m + 1:4 * m + 1]
+        req_idx = leaf_meta[4 * m + 1:5 * m + 1].long()
+        col_idx = leaf_meta[5 * m + 1:].long()
+        leaf_uniforms = torch.zeros((m, 2), dtype=torch.float32, device=device)
+        leaf_uniforms[:, 1] = uniforms[req_idx, col_idx]
+        leaf_head = ops.lm_head(hidden, weight, leaf_index)
+        leaf = ops.tree_sample_projected(leaf_head.logits, single_offset, single_parent,
+                                         single_token, leaf_uniforms, 0,
+                                         row_max=leaf_head.row_max, row_sum=leaf_head.row_sum)
+        leaf_host = torch.cat([leaf.bonus, leaf.accept_len, leaf.status,
+                               projection_valid(leaf_head)]).tolist()
+        if validate and leaf_host[-1] != 1:
+            raise FloatingPointError("Invalid lazy-projection leaf probabilities")
+        if leaf_host[-2] != 0 or any(v != 0 for v in leaf_host[m:2 * m]):
+            raise RuntimeError("HIP tree sampler returned invalid control values")
+        for i, bonus in zip(leaf_requests, leaf_host[:m]):
+            bonuses[i] = bonus
+
+    results = []
+    for i, ((parents, tokens, depth), accepted, bonus) in enumerate(
+            zip(topologies, lengths, bonuses)):
+        if not 0 <= accepted <= depth or not 0 <= bonus < vocab:
+            raise RuntimeError("HIP tree sampler returned invalid control values")
+        nodes = [int(v) for v in nodes_flat[i * width:i * width + accepted]]
+        if leaves[i] >= 0 and leaves[i] != (nodes[-1] if nodes else 0):
+            raise RuntimeError("HIP tree sampler returned an invalid leaf")
+        leaf_projected = int(leaves[i] >= 0)
+        results.append((nodes, [tokens[node - 1] for node in nodes], int(bonus), {
+            "internal_projected_rows": internal_counts[i],
+            "leaf_projected_rows": leaf_projected,
+            "projected_rows": internal_counts[i] + leaf_projected,
+            "total_tree_rows": rows[i],
+            "lm_head_rows": internal_counts[i] + leaf_projected,
+            "probability_rows": internal_counts[i] + leaf_projected,
+            "physical_internal_projection_rows": int(internal_rows.size),
+            "sparse_exit": True,
+        }))
+    return results

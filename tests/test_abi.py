@@ -20,7 +20,7 @@ def _declared_functions():
 
 def test_library_loads_and_struct_sizes_match():
     lib = _lib.load()
-    assert lib.sg_abi_version() == _lib.SG_ABI_VERSION == 3
+    assert lib.sg_abi_version() == _lib.SG_ABI_VERSION == 4
 
 
 def test_every_declared_symbol_is_exported():
@@ -193,6 +193,44 @@ def test_noalloc_sampler_rejects_oversized_waves_before_any_device_call():
     a.workspace_dev, a.workspace_bytes = 0, 0
     a.logits_dtype = 7
     assert lib.sg_tree_sample_noalloc(ctypes.byref(a), None) == _lib.SG_EINVAL
+
+
+def test_lm_head_and_projected_sampler_reject_bad_arguments_on_the_host():
+    lib = _lib.load()
+    assert lib.sg_lm_head_tile_count(151936) == 1187
+    assert lib.sg_lm_head_tile_count(129) == 2 and lib.sg_lm_head_tile_count(0) == -1
+    a = _lib.SgLmHeadArgs()
+    a.num_rows, a.hidden_size, a.vocab, a.num_hidden_rows = 4, 4096, 151936, 4
+    for name in ("hidden_dev", "weight_dev", "logits_dev", "tile_stats_dev", "row_max_dev",
+                 "row_sum_dev"):
+        setattr(a, name, 0x1000)
+    a.hidden_row_stride, a.weight_row_stride, a.logits_row_stride = 4096, 4096, 151936
+    for field, value, text in (("hidden_size", 4000, b"multiple of 64"),
+                               ("hidden_size", 32, b"multiple of 64"),
+                               ("vocab", 0, b"vocab"),
+                               ("logits_row_stride", 151930, b"strides")):
+        good = getattr(a, field)
+        setattr(a, field, value)
+        assert lib.sg_lm_head(ctypes.byref(a), None) == _lib.SG_EINVAL, field
+        assert text in lib.sg_last_error(), (field, lib.sg_last_error())
+        setattr(a, field, good)
+    a.hidden_dev = 0x1008  # not 16-byte aligned
+    assert lib.sg_lm_head(ctypes.byref(a), None) == _lib.SG_EINVAL
+    a.num_rows = 0         # nothing to project: no launch
+    assert lib.sg_lm_head(ctypes.byref(a), None) == _lib.SG_OK
+    s = _lib.SgTreeSampleArgs()
+    s.num_requests, s.num_rows, s.vocab, s.logits_row_stride, s.uniform_stride = 1, 4, 100, 100, 2
+    for name in ("logits_dev", "row_offset_dev", "parent_dev", "token_dev", "uniforms_dev",
+                 "row_max_dev", "row_sum_dev", "accept_len_dev", "bonus_dev"):
+        setattr(s, name, 0x1000)
+    s.workspace_dev, s.workspace_bytes = 0x1000, 1 << 20
+    s.logits_row_dev = 0x1000   # a row map without terminal_leaf_dev
+    assert lib.sg_tree_sample(ctypes.byref(s), None) == _lib.SG_EINVAL
+    assert b"terminal_leaf_dev" in lib.sg_last_error()
+    s.logits_row_dev, s.num_logits_rows = 0, 3  # logits rows differ without a map
+    assert lib.sg_tree_sample(ctypes.byref(s), None) == _lib.SG_EINVAL
+    s.num_logits_rows, s.flags = 0, 6
+    assert lib.sg_tree_sample(ctypes.byref(s), None) == _lib.SG_EINVAL
 
 
 def test_product_package_never_imports_the_oracle():
