@@ -21,6 +21,11 @@ Also reported in the same JSON line:
   tier128     a Qwen3-8B-shape wave of 128-node trees only (the MFMA-heaviest
               units), 4 rotating input sets;
   sampler     tree sampling over 64 x 32 nodes, vocab 151936 (nodes/s, GB/s);
+  lm_head     the lazy-projection LM head at the Qwen3-8B shape (H 4096, V
+              151936, bf16): the 752 internal rows of the measured wave, the
+              leaf pass (64 rows) and every row (2048), in TFLOP/s against the
+              2.5 PFLOP/s bf16 peak, beside the library GEMM (torch.matmul)
+              plus the separate statistics pass it would need;
   long_context the heterogeneous long-context wave (128 requests, prefixes
               log-uniform 8k-32k, 4096 rows): attention, commit, and tree
               sampling over fp32 logits of every packed row (one input set);
@@ -56,6 +61,7 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-sampler", action="store_true")
     p.add_argument("--no-long-context", action="store_true")
+    p.add_argument("--no-lm-head", action="store_true")
     p.add_argument("--target-units", type=int, default=0)
     p.add_argument("--counters-only", action="store_true",
                    help="for hardware-counter runs: --steps attention calls on the rotating "
@@ -234,6 +240,47 @@ def sampler_bench(torch, W, ops, device, iters, warmup):
     ms = time_calls(torch, call, iters)
     wl = sets[0]["wl"]
     return wl, ms, sets, b2b
+
+
+def lm_head_bench(torch, np, W, ops, device, iters=10, warmup=2):
+    """sg_lm_head at the Qwen3-8B head shape over the measured wave's rows."""
+    wl = W.qwen3_8b_workload()
+    hidden_size, vocab = 4096, 151936
+    gen = torch.Generator(device=device).manual_seed(77)
+    hidden = torch.randn((wl.total_rows, hidden_size), generator=gen,
+                         device=device).to(torch.bfloat16)
+    weight = (torch.randn((vocab, hidden_size), generator=gen, device=device)
+              * (2.0 / hidden_size ** 0.5)).to(torch.bfloat16)
+    internal = np.asarray([int(wl.row_offset[i]) + v for i, p in enumerate(wl.parents)
+                           for v in sorted(set(p[1:]))], np.int32)
+    leaves = np.asarray([int(wl.row_offset[i]) + len(p) - 1 for i, p in enumerate(wl.parents)],
+                        np.int32)
+    out = {"workload": f"{wl.name}: H {hidden_size}, V {vocab}, bf16 weight "
+                       f"{vocab * hidden_size * 2 / 1e9:.3f} GB",
+           "total_rows": wl.total_rows, "internal_rows": int(internal.size)}
+    for name, rows in (("internal", internal), ("leaf_pass", leaves),
+                       ("every_row", np.arange(wl.total_rows, dtype=np.int32))):
+        index = torch.from_numpy(rows).to(device)
+        for _ in range(warmup):
+            ops.lm_head(hidden, weight, index)
+        torch.cuda.synchronize()
+        ms = back_to_back(torch, lambda k: ops.lm_head(hidden, weight, index), iters)
+        flops = 2.0 * rows.size * hidden_size * vocab
+        line = {"rows": int(rows.size), "us_back_to_back": ms * 1e3,
+                "tflops": flops / (ms * 1e-3) / 1e12,
+                "frac": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS}
+        if name == "internal":
+            sel = hidden[index.long()].contiguous()
+            logits = torch.empty((rows.size, vocab), dtype=torch.bfloat16, device=device)
+            for _ in range(warmup):
+                torch.matmul(sel, weight.T, out=logits)
+            torch.cuda.synchronize()
+            gemm = back_to_back(torch, lambda k: torch.matmul(sel, weight.T, out=logits), iters)
+            stats = back_to_back(torch, lambda k: ops.row_stats(logits), iters)
+            line["library_gemm_us"] = gemm * 1e3
+            line["library_gemm_plus_stats_us"] = (gemm + stats) * 1e3
+        out[name] = line
+    return out
 
 
 def long_context_bench(torch, np, W, ops, device, iters=20, warmup=3):
@@ -550,6 +597,9 @@ def main():
             "frac": sbytes / (samp_b2b * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "algorithmic_bytes": sbytes,
         }
+    if not args.no_lm_head:
+        torch.cuda.empty_cache()
+        result["lm_head"] = lm_head_bench(torch, np, W, ops, device)
     if not args.no_long_context:
         torch.cuda.empty_cache()
         result["long_context"] = long_context_bench(torch, np, W, ops, device)

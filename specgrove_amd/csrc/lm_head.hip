@@ -40,6 +40,8 @@
 #pragma clang fp contract(off)
 
 #include <algorithm>
+#include <climits>
+#include <type_traits>
 
 #include "sg_common.h"
 #include "sg_math.h"
@@ -52,17 +54,29 @@ typedef __attribute__((ext_vector_type(16))) float floatx16;
 
 constexpr int kLmThreads = 256;
 constexpr int kTileV = 256;          // vocabulary tokens per workgroup tile
-constexpr int kTileR = 256;          // projected rows per workgroup tile
 constexpr int kStepK = 32;           // hidden dims per ring stage
 constexpr int kLmStages = 4;
-constexpr int kHalfTile = kTileV * kStepK * 2;  // bytes of one operand per stage (16 KiB)
-constexpr int kKbBytes = kHalfTile / 2;         // one 16-dim block of an operand
+constexpr int kWBytes = kTileV * kStepK * 2;  // weight bytes per stage (16 KiB)
+constexpr int kWKb = kWBytes / 2;             // one 16-dim block of the weight stage
 constexpr int kStatTokens = 128;     // tokens per statistics tile
 constexpr int kOutPitch = 2 * 128 + 16;  // LDS staging row: 128 bf16 + 16 bytes
 constexpr int kLmXcds = 8;
 constexpr int kMergeRowsPerBlock = 4;   // rows per 256-thread merge workgroup
 
-static_assert(kLmStages * 2 * kHalfTile <= 4 * 128 * kOutPitch, "staging covers the ring");
+// Row tile of R 32-row blocks per wave (64*R projected rows per workgroup):
+// R = 4 for waves of more than 128 rows, 2 up to 128, 1 up to 64 (the leaf
+// pass), so a small call does not multiply empty rows.
+template <int R>
+struct RowTile {
+  static constexpr int kRows = 64 * R;
+  static constexpr int kXBytes = kRows * kStepK * 2;   // hidden bytes per stage
+  static constexpr int kXKb = kXBytes / 2;
+  static constexpr int kStage = kWBytes + kXBytes;
+  static constexpr int kDmas = 4 + R;                  // copies per wave per stage
+  static constexpr int kStaging = 4 * 32 * R * kOutPitch;
+  static constexpr int kLds = kLmStages * kStage > kStaging ? kLmStages * kStage : kStaging;
+  static constexpr int kBlocksPerCU = R == 1 ? 2 : 1;
+};
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return static_cast<uint32_t>(
@@ -112,9 +126,11 @@ __device__ __forceinline__ bool tile_of(int b, int v_tiles, int r_tiles, int& vt
   return vt < v_tiles;
 }
 
-__global__ __launch_bounds__(kLmThreads, 1) void lm_head_kernel(SgLmHeadArgs a, int v_tiles,
-                                                                 int r_tiles) {
-  __shared__ __align__(1024) unsigned char smem[4 * 128 * kOutPitch];
+template <int R>
+__global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_kernel(
+    SgLmHeadArgs a, int v_tiles, int r_tiles) {
+  using T = RowTile<R>;
+  __shared__ __align__(1024) unsigned char smem[T::kLds];
   int vt, rt;
   if (!tile_of(blockIdx.x, v_tiles, r_tiles, vt, rt)) return;
   const int tid = threadIdx.x;
@@ -124,15 +140,17 @@ __global__ __launch_bounds__(kLmThreads, 1) void lm_head_kernel(SgLmHeadArgs a, 
   const int col = lane & 31;
   const int V = a.vocab;
   const int v0 = vt * kTileV;
-  const int r0 = rt * kTileR;
+  const int r0 = rt * T::kRows;
 
-  // DMA slots: per stage each operand is 16 instructions of 1 KiB; wave w
-  // issues instructions 4w .. 4w+3 of both.  Instruction q covers 16-dim block
-  // q >> 3 and tile rows 32*(q & 7) .. +31; lane i moves row 32*(q&7) + i/2,
-  // dims 8*(i&1) .. +7 of that block.  LDS layout of an operand stage:
-  // [16-dim block][256 rows][16 dims], so the MFMA reads below are 1 KiB
-  // contiguous per instruction (no bank conflicts).
-  uint32_t w_off[4], x_off[4], lds_off[4];
+  // DMA slots.  Per stage the weight is 16 copies of 1 KiB (wave w issues
+  // 4w .. 4w+3) and the hidden rows 4R (wave w issues Rw .. Rw+R-1).  Copy q
+  // of an operand covers 16-dim block q / (rows/32) and 32-row block
+  // q % (rows/32); lane i moves row 32*(q % (rows/32)) + i%32, dims 8*(i/32)
+  // .. +7 of that block.  LDS layout of an operand stage: [16-dim block]
+  // [32-row block][8-dim half][32 rows][8 dims], which is the MFMA operand
+  // layout itself: lane l's fragment of a 32-row block is the 16 bytes at
+  // 16*l, so every fragment read is one linear 1 KiB (no bank conflicts).
+  uint32_t w_off[4], w_lds[4], x_off[R], x_lds[R];
   const unsigned char* wbase =
       static_cast<const unsigned char*>(a.weight_dev) + static_cast<int64_t>(v0) * a.weight_row_stride * 2;
   const unsigned char* xbase = static_cast<const unsigned char*>(a.hidden_dev);
@@ -140,13 +158,21 @@ __global__ __launch_bounds__(kLmThreads, 1) void lm_head_kernel(SgLmHeadArgs a, 
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int q = wave * 4 + i;
-    const int kb = q >> 3;
-    const int row = 32 * (q & 7) + (lane >> 1);
-    const int dim = 16 * kb + 8 * (lane & 1);
+    const int row = 32 * (q & 7) + (lane & 31);
+    const int dim = 16 * (q >> 3) + 8 * (lane >> 5);
     // Tokens past the vocabulary re-read the last token (finite data the
-    // epilogue drops); rows past the projected rows re-read a valid row.
+    // epilogue drops).
     const int tok = min(v0 + row, V - 1) - v0;
     w_off[i] = static_cast<uint32_t>((static_cast<int64_t>(tok) * a.weight_row_stride + dim) * 2);
+    w_lds[i] = static_cast<uint32_t>((q >> 3) * kWKb + 1024 * (q & 7));
+  }
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int q = wave * R + i;
+    const int blocks = 2 * R;  // 32-row blocks of the row tile
+    const int row = 32 * (q % blocks) + (lane & 31);
+    const int dim = 16 * (q / blocks) + 8 * (lane >> 5);
+    // Rows past the projected rows re-read a valid row.
     const int prow = min(r0 + row, a.num_rows - 1);
     int src = a.row_index_dev != nullptr ? a.row_index_dev[prow] : prow;
     if (src < 0 || src >= a.num_hidden_rows) {
@@ -154,53 +180,53 @@ __global__ __launch_bounds__(kLmThreads, 1) void lm_head_kernel(SgLmHeadArgs a, 
       src = 0;
     }
     x_off[i] = static_cast<uint32_t>((static_cast<int64_t>(src) * a.hidden_row_stride + dim) * 2);
-    lds_off[i] = static_cast<uint32_t>(kb * kKbBytes + 1024 * (q & 7));
+    x_lds[i] = static_cast<uint32_t>(kWBytes + (q / blocks) * T::kXKb + 1024 * (q % blocks));
   }
   if (bad_index && a.status_dev != nullptr) atomicExch(a.status_dev, SG_EINVAL);
 
   const uint32_t ring = lds_addr(smem);
   const int steps = a.hidden_size / kStepK;
   auto issue = [&](int s) {
-    const uint32_t stage = ring + (s % kLmStages) * 2 * kHalfTile;
+    const uint32_t stage = ring + (s % kLmStages) * T::kStage;
     const unsigned char* wk = wbase + static_cast<int64_t>(s) * kStepK * 2;
     const unsigned char* xk = xbase + static_cast<int64_t>(s) * kStepK * 2;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(wk, w_off[i], stage + lds_off[i]);
+    for (int i = 0; i < 4; ++i) dma16(wk, w_off[i], stage + w_lds[i]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(xk, x_off[i], stage + kHalfTile + lds_off[i]);
+    for (int i = 0; i < R; ++i) dma16(xk, x_off[i], stage + x_lds[i]);
   };
 
-  floatx16 acc[4][4];
+  floatx16 acc[4][R];
 #pragma unroll
   for (int vb = 0; vb < 4; ++vb)
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
+    for (int rb = 0; rb < R; ++rb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[vb][rb][r] = 0.0f;
 
   const int wv = wave & 1;   // vocabulary half of the tile
   const int wr = wave >> 1;  // row half of the tile
-  const int a_lane = (wv * 128 + col) * 32 + 16 * half;
-  const int b_lane = (wr * 128 + col) * 32 + 16 * half;
+  const int a_lane = wv * 4 * 1024 + 16 * lane;  // first of this wave's 32-row blocks
+  const int b_lane = wr * R * 1024 + 16 * lane;
 
   // Operand fragments of one stage: weight rows (A) and hidden rows (B) of
   // both 16-dim blocks, read from LDS one stage ahead of their MFMAs.
   struct Frags {
     bf16x8 w[2][4];
-    bf16x8 x[2][4];
+    bf16x8 x[2][R];
   };
   auto load_frags = [&](int s, Frags& f) {
-    const unsigned char* st = smem + (s % kLmStages) * 2 * kHalfTile;
+    const unsigned char* st = smem + (s % kLmStages) * T::kStage;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
       for (int vb = 0; vb < 4; ++vb)
         f.w[kb][vb] =
-            as_bf16x8(*reinterpret_cast<const uint4*>(st + kb * kKbBytes + a_lane + vb * 1024));
+            as_bf16x8(*reinterpret_cast<const uint4*>(st + kb * kWKb + a_lane + vb * 1024));
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb)
-        f.x[kb][rb] = as_bf16x8(
-            *reinterpret_cast<const uint4*>(st + kHalfTile + kb * kKbBytes + b_lane + rb * 1024));
+      for (int rb = 0; rb < R; ++rb)
+        f.x[kb][rb] = as_bf16x8(*reinterpret_cast<const uint4*>(
+            st + kWBytes + kb * T::kXKb + b_lane + rb * 1024));
     }
   };
   auto mma = [&](const Frags& f) {
@@ -209,7 +235,7 @@ __global__ __launch_bounds__(kLmThreads, 1) void lm_head_kernel(SgLmHeadArgs a, 
 #pragma unroll
       for (int vb = 0; vb < 4; ++vb)
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb)
+        for (int rb = 0; rb < R; ++rb)
           acc[vb][rb] =
               __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.w[kb][vb], f.x[kb][rb], acc[vb][rb], 0, 0, 0);
   };
@@ -219,9 +245,9 @@ __global__ __launch_bounds__(kLmThreads, 1) void lm_head_kernel(SgLmHeadArgs a, 
   auto open_stage = [&](int s) {
     const int newer = min(kLmStages - 2, steps - 1 - s);
     if (newer >= 2) {
-      __builtin_amdgcn_s_waitcnt(vmcnt_encoding(16));
+      __builtin_amdgcn_s_waitcnt(vmcnt_encoding(2 * T::kDmas));
     } else if (newer == 1) {
-      __builtin_amdgcn_s_waitcnt(vmcnt_encoding(8));
+      __builtin_amdgcn_s_waitcnt(vmcnt_encoding(T::kDmas));
     } else {
       __builtin_amdgcn_s_waitcnt(vmcnt_encoding(0));
     }
@@ -252,15 +278,15 @@ __global__ __launch_bounds__(kLmThreads, 1) void lm_head_kernel(SgLmHeadArgs a, 
   __syncthreads();  // the ring is free: it becomes the output staging area
 
   // Epilogue.  acc[vb][rb][r] holds token v0 + 128*wv + 32*vb + 8*(r/4) +
-  // 4*half + r%4 of tile row 128*wr + 32*rb + col.
+  // 4*half + r%4 of tile row 32*R*wr + 32*rb + col.
   const int tok0 = v0 + 128 * wv;           // first token of this wave's statistics tile
   const bool tile_live = tok0 < V;
   const int n_tiles = (V + kStatTokens - 1) / kStatTokens;
-  unsigned char* stage = smem + wave * 128 * kOutPitch;
+  unsigned char* stage = smem + wave * 32 * R * kOutPitch;
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb) {
-    const int row_local = 32 * rb + col;       // row inside this wave's 128 rows
-    const int row = r0 + 128 * wr + row_local;  // projected row
+  for (int rb = 0; rb < R; ++rb) {
+    const int row_local = 32 * rb + col;          // row inside this wave's 32*R rows
+    const int row = r0 + 32 * R * wr + row_local;  // projected row
     float x[64];
     float m = -__builtin_inff();
 #pragma unroll
@@ -307,9 +333,9 @@ __global__ __launch_bounds__(kLmThreads, 1) void lm_head_kernel(SgLmHeadArgs a, 
   if (!tile_live) return;
   uint16_t* out = static_cast<uint16_t*>(a.logits_dev);
 #pragma unroll 4
-  for (int i = 0; i < 32; ++i) {
+  for (int i = 0; i < 8 * R; ++i) {
     const int row_local = 4 * i + (lane >> 4);
-    const int row = r0 + 128 * wr + row_local;
+    const int row = r0 + 32 * R * wr + row_local;
     const int chunk = lane & 15;
     const int tok = tok0 + 8 * chunk;
     const uint4 v = *reinterpret_cast<const uint4*>(stage + row_local * kOutPitch + 16 * chunk);
@@ -389,14 +415,22 @@ extern "C" int sg_lm_head(const SgLmHeadArgs* args, sg_stream_t stream) {
   SG_REQUIRE(static_cast<int64_t>(a.num_hidden_rows) * a.hidden_row_stride * 2 < (int64_t{1} << 32),
              "hidden matrix above 4 GiB");
   const int v_tiles = (a.vocab + kTileV - 1) / kTileV;
-  const int r_tiles = (a.num_rows + kTileR - 1) / kTileR;
-  const int64_t blocks =
-      static_cast<int64_t>((v_tiles + kLmXcds - 1) / kLmXcds) * kLmXcds * r_tiles;
-  SG_REQUIRE(blocks < INT32_MAX, "wave too large");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  lm_head_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kLmThreads), 0, s>>>(a, v_tiles,
-                                                                                  r_tiles);
-  SG_LAUNCH_CHECK();
+  auto launch = [&](auto tag) -> int {
+    constexpr int R = decltype(tag)::value;
+    const int r_tiles = (a.num_rows + RowTile<R>::kRows - 1) / RowTile<R>::kRows;
+    const int64_t blocks =
+        static_cast<int64_t>((v_tiles + kLmXcds - 1) / kLmXcds) * kLmXcds * r_tiles;
+    SG_REQUIRE(blocks < INT32_MAX, "wave too large");
+    lm_head_kernel<R><<<dim3(static_cast<unsigned>(blocks)), dim3(kLmThreads), 0, s>>>(
+        a, v_tiles, r_tiles);
+    SG_LAUNCH_CHECK();
+    return SG_OK;
+  };
+  const int rc = a.num_rows <= 64    ? launch(std::integral_constant<int, 1>{})
+                 : a.num_rows <= 128 ? launch(std::integral_constant<int, 2>{})
+                                     : launch(std::integral_constant<int, 4>{});
+  if (rc != SG_OK) return rc;
   const int merge_blocks = (a.num_rows + kMergeRowsPerBlock - 1) / kMergeRowsPerBlock;
   lm_head_rows_kernel<<<dim3(merge_blocks), dim3(kMergeRowsPerBlock * kWave), 0, s>>>(a);
   SG_LAUNCH_CHECK();
