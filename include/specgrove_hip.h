@@ -338,9 +338,81 @@ int sg_lm_head(const SgLmHeadArgs* args, sg_stream_t stream);
 /* 128-token statistics tiles per row: ceil(V / 128), or -1 for V < 1. */
 int64_t sg_lm_head_tile_count(int32_t vocab);
 
+/* ------------------------------------------------------------------------
+ * (E) Target decoder layer stack: the fused elementwise stages between the
+ * library projections (Qwen3 family).
+ *
+ * Replace the transformers decoder layers the reference runs through
+ * Engine.target_hidden_forward (engine.py:499-517; transformers==4.57.1 per
+ * requirements-experiment.txt: Qwen3RMSNorm, Qwen3Attention's q_norm/k_norm
+ * and apply_rotary_pos_emb, Qwen3MLP's act_fn(gate) * up) and the draft
+ * feature gather of the kept rows (CTBD:2144-2158).  bf16 in and out, fp32
+ * inside, with the modules' bf16 rounding points.
+ * ---------------------------------------------------------------------- */
+typedef struct SgAddRmsNormArgs {
+  int32_t num_rows;
+  int32_t hidden;                /* multiple of 8, at most 8192 */
+  float eps;
+  int32_t reserved;
+  const void* x_dev;             /* bf16 [R, x_stride] */
+  int64_t x_stride;
+  const void* residual_dev;      /* optional bf16 [R, residual_stride], added to x first */
+  int64_t residual_stride;
+  const void* weight_dev;        /* bf16 [hidden] */
+  void* out_dev;                 /* bf16 [R, out_stride]: RMSNorm(x + residual) */
+  int64_t out_stride;
+  void* residual_out_dev;        /* optional bf16 [R, residual_out_stride]: x + residual */
+  int64_t residual_out_stride;
+} SgAddRmsNormArgs;
+
+/* out = weight * bf16((x + residual) * rsqrt(mean((x + residual)^2) + eps)),
+ * with x + residual rounded to bf16 first (the decoder's residual stream). */
+int sg_add_rmsnorm(const SgAddRmsNormArgs* args, sg_stream_t stream);
+
+typedef struct SgQkNormRopeArgs {
+  int32_t num_rows;
+  int32_t num_q_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;              /* 64 or 128 */
+  float eps;
+  int32_t reserved;
+  const void* qkv_dev;           /* bf16 [R, qkv_row_stride]: Hq q heads, Hkv k heads,
+                                    Hkv v heads of D each (the merged projection) */
+  int64_t qkv_row_stride;
+  const void* q_norm_dev;        /* bf16 [D] */
+  const void* k_norm_dev;        /* bf16 [D] */
+  const float* inv_freq_dev;     /* [D/2] rotary inverse frequencies */
+  const int64_t* positions_dev;  /* [R] */
+  void* q_out_dev;               /* bf16 [R, q_row_stride] as [Hq, D] per row */
+  int64_t q_row_stride;
+  void* k_out_dev;               /* bf16 [Hkv, kv_head_stride] as [R, D] per head */
+  void* v_out_dev;
+  int64_t kv_head_stride;
+} SgQkNormRopeArgs;
+
+/* Per-head RMSNorm of q and k, rotary embedding of both (rotate-half form,
+ * bf16 cos/sin of fp32 angles position * inv_freq), v copied. */
+int sg_qk_norm_rope(const SgQkNormRopeArgs* args, sg_stream_t stream);
+
+/* out[r, :I] = bf16(bf16(silu(gate)) * up) with gate = gate_up[r, :I] and
+ * up = gate_up[r, I:2I] (Qwen3MLP act_fn(gate_proj(x)) * up_proj(x)). */
+int sg_silu_mul(const void* gate_up_dev, int64_t gate_up_row_stride, int32_t num_rows,
+                int32_t intermediate, void* out_dev, int64_t out_row_stride,
+                sg_stream_t stream);
+
+/* Draft features of the kept rows (CTBD:2144-2158): out[k, l*width ..] =
+ * src_dev[l][index_dev[k], :width] for l < num_src, i.e. the kept rows of
+ * several layers' hidden states concatenated along the feature dimension.
+ * src_dev is a device array of num_src device pointers; an index outside
+ * [0, num_src_rows) writes zeros and sets *status_dev (optional) to SG_EINVAL. */
+int sg_gather_rows(const void* const* src_dev, int32_t num_src, int64_t src_row_stride,
+                   int32_t width, int32_t num_src_rows, const int32_t* index_dev,
+                   int32_t num_index, void* out_dev, int64_t out_row_stride,
+                   int32_t* status_dev, sg_stream_t stream);
+
 /* sizeof() of the argument structs as compiled into the library, for binding
  * checks: which = 0 SgTreeAttnArgs, 1 SgKvCommitArgs, 2 SgTreeSampleArgs,
- * 3 SgKvSplitArgs, 4 SgLmHeadArgs.
+ * 3 SgKvSplitArgs, 4 SgLmHeadArgs, 5 SgAddRmsNormArgs, 6 SgQkNormRopeArgs.
  * Returns -1 for an unknown index.  No reference counterpart. */
 int64_t sg_abi_struct_size(int32_t which);
 

@@ -110,12 +110,34 @@ class SgLmHeadArgs(ctypes.Structure):
     ]
 
 
+class SgAddRmsNormArgs(ctypes.Structure):
+    _fields_ = [
+        ("num_rows", c_i32), ("hidden", c_i32), ("eps", c_f32), ("reserved", c_i32),
+        ("x_dev", c_void_p), ("x_stride", c_i64),
+        ("residual_dev", c_void_p), ("residual_stride", c_i64),
+        ("weight_dev", c_void_p), ("out_dev", c_void_p), ("out_stride", c_i64),
+        ("residual_out_dev", c_void_p), ("residual_out_stride", c_i64),
+    ]
+
+
+class SgQkNormRopeArgs(ctypes.Structure):
+    _fields_ = [
+        ("num_rows", c_i32), ("num_q_heads", c_i32), ("num_kv_heads", c_i32),
+        ("head_dim", c_i32), ("eps", c_f32), ("reserved", c_i32),
+        ("qkv_dev", c_void_p), ("qkv_row_stride", c_i64),
+        ("q_norm_dev", c_void_p), ("k_norm_dev", c_void_p), ("inv_freq_dev", c_void_p),
+        ("positions_dev", c_void_p), ("q_out_dev", c_void_p), ("q_row_stride", c_i64),
+        ("k_out_dev", c_void_p), ("v_out_dev", c_void_p), ("kv_head_stride", c_i64),
+    ]
+
+
 EXPORTED_SYMBOLS = (
     "sg_abi_version", "sg_last_error", "sg_abi_struct_size",
     "sg_tree_attn_plan", "sg_tree_attn_fwd", "sg_kv_commit",
     "sg_tree_sample", "sg_tree_sample_workspace_bytes", "sg_row_stats", "sg_exp_probe",
     "sg_tree_sample_noalloc", "sg_tree_attn_plan_check", "sg_kv_split",
     "sg_lm_head", "sg_lm_head_tile_count",
+    "sg_add_rmsnorm", "sg_qk_norm_rope", "sg_silu_mul", "sg_gather_rows",
 )
 
 # Static scratch of sg_tree_sample_noalloc (SG_TREE_SAMPLE_NOALLOC_SCRATCH_BYTES).
@@ -171,6 +193,15 @@ def load() -> ctypes.CDLL:
     lib.sg_lm_head.argtypes = [ctypes.POINTER(SgLmHeadArgs), c_void_p]
     lib.sg_lm_head_tile_count.restype = c_i64
     lib.sg_lm_head_tile_count.argtypes = [c_i32]
+    lib.sg_add_rmsnorm.restype = c_i32
+    lib.sg_add_rmsnorm.argtypes = [ctypes.POINTER(SgAddRmsNormArgs), c_void_p]
+    lib.sg_qk_norm_rope.restype = c_i32
+    lib.sg_qk_norm_rope.argtypes = [ctypes.POINTER(SgQkNormRopeArgs), c_void_p]
+    lib.sg_silu_mul.restype = c_i32
+    lib.sg_silu_mul.argtypes = [c_void_p, c_i64, c_i32, c_i32, c_void_p, c_i64, c_void_p]
+    lib.sg_gather_rows.restype = c_i32
+    lib.sg_gather_rows.argtypes = [c_void_p, c_i32, c_i64, c_i32, c_i32, c_void_p, c_i32,
+                                   c_void_p, c_i64, c_void_p, c_void_p]
     lib.sg_exp_probe.restype = c_i32
     lib.sg_exp_probe.argtypes = [c_void_p, c_void_p, c_i64, c_void_p]
     version = lib.sg_abi_version()
@@ -179,7 +210,7 @@ def load() -> ctypes.CDLL:
                            f"version {SG_ABI_VERSION}; rebuild with `python -m "
                            f"specgrove_amd.build`")
     expected = {0: SgTreeAttnArgs, 1: SgKvCommitArgs, 2: SgTreeSampleArgs, 3: SgKvSplitArgs,
-                4: SgLmHeadArgs}
+                4: SgLmHeadArgs, 5: SgAddRmsNormArgs, 6: SgQkNormRopeArgs}
     for which, struct in expected.items():
         size = lib.sg_abi_struct_size(which)
         if size != ctypes.sizeof(struct):

@@ -29,6 +29,8 @@ extern "C" int64_t sg_abi_struct_size(int32_t which) {
     case 2: return static_cast<int64_t>(sizeof(SgTreeSampleArgs));
     case 3: return static_cast<int64_t>(sizeof(SgKvSplitArgs));
     case 4: return static_cast<int64_t>(sizeof(SgLmHeadArgs));
+    case 5: return static_cast<int64_t>(sizeof(SgAddRmsNormArgs));
+    case 6: return static_cast<int64_t>(sizeof(SgQkNormRopeArgs));
     default: return -1;
   }
 }
