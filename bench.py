@@ -21,6 +21,10 @@ Also reported in the same JSON line:
   tier128     a Qwen3-8B-shape wave of 128-node trees only (the MFMA-heaviest
               units), 4 rotating input sets;
   sampler     tree sampling over 64 x 32 nodes, vocab 151936 (nodes/s, GB/s);
+  layer       one Qwen3-8B decoder layer on the HIP stack over the measured
+              wave (2048 rows, random weights): the whole layer and each of
+              its fused elementwise kernels (GB/s against 8 TB/s) and library
+              projections (TFLOP/s);
   lm_head     the lazy-projection LM head at the Qwen3-8B shape (H 4096, V
               151936, bf16): the 752 internal rows of the measured wave, the
               leaf pass (64 rows) and every row (2048), in TFLOP/s against the
@@ -62,14 +66,17 @@ def parse_args():
     p.add_argument("--no-sampler", action="store_true")
     p.add_argument("--no-long-context", action="store_true")
     p.add_argument("--no-lm-head", action="store_true")
+    p.add_argument("--no-layer", action="store_true")
     p.add_argument("--target-units", type=int, default=0)
     p.add_argument("--counters-only", action="store_true",
                    help="for hardware-counter runs: --steps attention calls on the rotating "
                         "input sets, then one 1 GiB device copy whose counter readings "
                         "calibrate FETCH_SIZE / WRITE_SIZE; prints nothing")
     p.add_argument("--counters-workload", default="qwen3_8b",
-                   choices=["qwen3_8b", "qwen3_4b", "tier128", "long_context"],
-                   help="the attention wave of a --counters-only run")
+                   choices=["qwen3_8b", "qwen3_4b", "tier128", "long_context", "lm_head",
+                            "layer"],
+                   help="what a --counters-only run repeats: an attention wave, the LM "
+                        "head over the Qwen3-8B wave's internal rows, or one decoder layer")
     return p.parse_args()
 
 
@@ -242,8 +249,88 @@ def sampler_bench(torch, W, ops, device, iters, warmup):
     return wl, ms, sets, b2b
 
 
-def lm_head_bench(torch, np, W, ops, device, iters=10, warmup=2):
-    """sg_lm_head at the Qwen3-8B head shape over the measured wave's rows."""
+def layer_bench(torch, np, W, ops, device, iters=20, warmup=3):
+    """One Qwen3-8B decoder layer (hidden 4096, 32 q / 8 kv heads, D 128,
+    intermediate 12288) on Qwen3TargetStack over the measured wave."""
+    from types import SimpleNamespace
+    from specgrove_amd import attention, target
+    wl = W.qwen3_8b_workload()
+    hid, inter, hq, hkv, d = 4096, 12288, wl.num_q_heads, wl.num_kv_heads, wl.head_dim
+    rows = wl.total_rows
+    gen = torch.Generator(device=device).manual_seed(91)
+
+    def rnd(*shape, scale=1.0):
+        return (torch.randn(shape, generator=gen, device=device) * scale).to(torch.bfloat16)
+
+    layer = target._Layer(
+        ln1=rnd(hid, scale=0.1) + 1, wqkv=rnd((hq + 2 * hkv) * d, hid, scale=hid ** -0.5),
+        q_norm=rnd(d, scale=0.1) + 1, k_norm=rnd(d, scale=0.1) + 1,
+        wo=rnd(hid, hq * d, scale=(hq * d) ** -0.5), ln2=rnd(hid, scale=0.1) + 1,
+        wgu=rnd(2 * inter, hid, scale=hid ** -0.5), wd=rnd(hid, inter, scale=inter ** -0.5))
+    stack = target.Qwen3TargetStack(
+        embed=rnd(4096, hid), layers=[layer], norm=rnd(hid, scale=0.1) + 1,
+        lm_head=rnd(8, hid), num_q_heads=hq, num_kv_heads=hkv, head_dim=d, rope_theta=1e6,
+        eps=1e-6)
+    q, kc, vc, kt, vt = wl.make_tensors(device, seed=321)
+    del q, kt, vt
+    pool = SimpleNamespace(key_storage=[kc], value_storage=[vc])
+    mask = attention.PackedTreeMask(
+        pool=pool, row_offset=torch.from_numpy(wl.row_offset).to(device),
+        parent=torch.from_numpy(wl.parent_flat).to(device),
+        prefix_start=torch.from_numpy(wl.prefix_start).to(device),
+        prefix_len=torch.from_numpy(wl.prefix_len.astype(np.int32)).to(device),
+        row_offset_host=wl.row_offset, prefix_len_host=wl.prefix_len.astype(np.int32))
+
+    class _Rows:
+        def update(self, k, v, layer_idx):
+            return k, v
+
+    ids = torch.randint(0, 4096, (1, rows), generator=gen, device=device)
+    depths = np.concatenate([W.depths_of(p) for p in wl.parents])
+    positions = torch.from_numpy(np.repeat(wl.prefix_len, wl.rows) + depths).to(device)[None]
+    x = rnd(rows, hid)
+    res = rnd(rows, hid)
+    qkv = rnd(rows, (hq + 2 * hkv) * d)
+    gu = rnd(rows, 2 * inter)
+    h = rnd(rows, hid)
+    act = rnd(rows, inter)
+    pos = positions.reshape(-1).contiguous()
+    parts = {
+        "add_rmsnorm": (lambda k: target.add_rmsnorm(x, layer.ln1, 1e-6, res, want_sum=True),
+                        4 * rows * hid * 2, 0),
+        "qk_norm_rope": (lambda k: target.qk_norm_rope(qkv, hq, hkv, d, layer.q_norm,
+                                                       layer.k_norm, stack.inv_freq, pos, 1e-6),
+                         2 * rows * (hq + 2 * hkv) * d * 2, 0),
+        "silu_mul": (lambda k: target.silu_mul(gu), rows * 3 * inter * 2, 0),
+        "qkv_proj": (lambda k: torch.matmul(h, layer.wqkv.T), 0,
+                     2 * rows * hid * (hq + 2 * hkv) * d),
+        "o_proj": (lambda k: torch.matmul(h, layer.wo.T), 0, 2 * rows * hid * hq * d),
+        "gate_up_proj": (lambda k: torch.matmul(h, layer.wgu.T), 0, 2 * rows * hid * 2 * inter),
+        "down_proj": (lambda k: torch.matmul(act, layer.wd.T), 0, 2 * rows * hid * inter),
+        "layer": (lambda k: stack.forward(input_ids=ids, position_ids=positions,
+                                          attention_mask=mask, past_key_values=_Rows()), 0, 0),
+    }
+    out = {"workload": f"{wl.name}: one Qwen3-8B layer (hidden {hid}, {hq} q / {hkv} kv "
+                       f"heads, D {d}, intermediate {inter}), random bf16 weights",
+           "rows": rows}
+    for name, (fn, nbytes, flops) in parts.items():
+        for k in range(warmup):
+            fn(k)
+        torch.cuda.synchronize()
+        ms = back_to_back(torch, fn, iters)
+        line = {"us": ms * 1e3}
+        if nbytes:
+            line["gbs"] = nbytes / (ms * 1e-3) / 1e9
+            line["frac"] = line["gbs"] / HBM_PEAK_GBS
+        if flops:
+            line["tflops"] = flops / (ms * 1e-3) / 1e12
+        out[name] = line
+    return out
+
+
+def lm_head_inputs(torch, np, W, device):
+    """The Qwen3-8B wave's final hidden rows (random), a Qwen3-8B-shaped head
+    weight (random), and the wave's internal rows and one leaf per request."""
     wl = W.qwen3_8b_workload()
     hidden_size, vocab = 4096, 151936
     gen = torch.Generator(device=device).manual_seed(77)
@@ -255,6 +342,13 @@ def lm_head_bench(torch, np, W, ops, device, iters=10, warmup=2):
                            for v in sorted(set(p[1:]))], np.int32)
     leaves = np.asarray([int(wl.row_offset[i]) + len(p) - 1 for i, p in enumerate(wl.parents)],
                         np.int32)
+    return wl, hidden, weight, internal, leaves
+
+
+def lm_head_bench(torch, np, W, ops, device, iters=10, warmup=2):
+    """sg_lm_head at the Qwen3-8B head shape over the measured wave's rows."""
+    wl, hidden, weight, internal, leaves = lm_head_inputs(torch, np, W, device)
+    hidden_size, vocab = weight.shape[1], weight.shape[0]
     out = {"workload": f"{wl.name}: H {hidden_size}, V {vocab}, bf16 weight "
                        f"{vocab * hidden_size * 2 / 1e9:.3f} GB",
            "total_rows": wl.total_rows, "internal_rows": int(internal.size)}
@@ -449,7 +543,19 @@ def read_traffic():
 
 
 def counters_only(torch, np, W, ops, device, steps, warmup, workload="qwen3_8b"):
-    """Attention calls plus a copy of known size, for rocprofv3 --pmc runs."""
+    """Attention calls (or LM head / decoder layer calls) plus a copy of known
+    size, for rocprofv3 --pmc runs."""
+    if workload == "lm_head":
+        _, hidden, weight, internal, _ = lm_head_inputs(torch, np, W, device)
+        index = torch.from_numpy(internal).to(device)
+        for _ in range(warmup + steps):
+            ops.lm_head(hidden, weight, index)
+        torch.cuda.synchronize()
+        return
+    if workload == "layer":
+        layer_bench(torch, np, W, ops, device, iters=steps, warmup=warmup)
+        torch.cuda.synchronize()
+        return
     make = {"qwen3_8b": W.qwen3_8b_workload, "qwen3_4b": W.qwen3_4b_workload,
             "tier128": W.tier128_workload, "long_context": W.long_context_workload}[workload]
     sets_n = 1 if workload == "long_context" else N_SETS
@@ -600,6 +706,9 @@ def main():
     if not args.no_lm_head:
         torch.cuda.empty_cache()
         result["lm_head"] = lm_head_bench(torch, np, W, ops, device)
+    if not args.no_layer:
+        torch.cuda.empty_cache()
+        result["layer"] = layer_bench(torch, np, W, ops, device)
     if not args.no_long_context:
         torch.cuda.empty_cache()
         result["long_context"] = long_context_bench(torch, np, W, ops, device)
