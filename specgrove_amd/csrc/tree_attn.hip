@@ -15,13 +15,14 @@
 //   work list = the units one workgroup runs in order; by default one unit,
 //               largest first, so that the hardware dispatcher balances the
 //               end of the launch;
-//   window    = one barrier; consumes one group of 32-key K and V tiles, moved
+//   window    = one barrier; consumes two 32-key K and V tiles, moved
 //               HBM -> LDS by global_load_lds_dwordx4 (no register staging)
-//               into 4-tile rings issued two to four windows ahead;
-//   wave      = one q-group over every tile (3-4 q-groups) or one of two key
-//               streams of a q-group taking alternate tiles (1-2 q-groups).
-//               Every wave runs its own online softmax; the key streams of a
-//               q-group are merged through LDS at the end of the unit.
+//               into 4-tile rings issued one window ahead;
+//   wave      = one q-group over both tiles of every window (3-4 q-groups)
+//               or one of two key streams of a q-group taking one tile of
+//               each window (1-2 q-groups).  Every wave runs its own online
+//               softmax; the key streams of a q-group are merged through LDS
+//               at the end of the unit.
 // Per 32-key block a wave computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16
 // (A = K rows from LDS stored in the permuted order pi, so the result gives
 // each lane 16 consecutive keys; B = Q in registers) and O^T += V^T P^T with
@@ -51,8 +52,7 @@ typedef __attribute__((address_space(3))) short4_t lds_short4;
 
 constexpr int kThreads = 256;
 constexpr int kQPerUnit = 128;
-constexpr int kTileKeys = 32;
-constexpr int kBlocksPerTile = kTileKeys / 32;  // 32-key MFMA blocks per tile
+constexpr int kTileKeys = 32;                   // keys per tile: one 32-key MFMA block
 constexpr int kListsPerCU = 2;                  // resident workgroups per CU
 constexpr int kStages = 4;
 constexpr int kWaves = 4;
@@ -300,18 +300,17 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
   const int half = lane >> 5;
   const int col = lane & 31;
   const int nq = (u.row_count * G + 31) / 32;   // q-groups in use, 1..4
-  // Waves sharing a q-group ("key streams"): 4 when the unit has 1-2 q-groups
-  // (they take the four 32-key blocks of two consecutive tiles), else 2 (the
-  // two blocks of one tile).  Every wave handles one 32-key block per
-  // iteration.  Waves beyond nq*streams repeat stream 0's work on the same
-  // LDS data and discard it.
+  // Every window (one barrier) consumes two consecutive 32-key tiles.  With
+  // 1-2 q-groups two waves share a q-group ("key streams") and take one tile
+  // each; their results are merged at the end of the unit.  With 3-4 q-groups
+  // every wave takes both tiles, one after the other.  Waves beyond
+  // nq*streams repeat stream 0's work on the same LDS data and discard it.
   const int streams = nq <= 2 ? 2 : 1;
-  const int per_iter = streams / kBlocksPerTile;  // tiles consumed per iteration
+  const bool both = streams == 1;
   const int qg = wave % nq;
   const int ks = wave / nq;                     // key stream of this wave
   const bool active = ks < streams;
-  const int my_tile = active ? ks / kBlocksPerTile : 0;  // tile of the window this wave takes
-  const int my_blk = active ? ks % kBlocksPerTile : 0;   // 32-key block inside that tile
+  const int my_tile = active ? ks : 0;          // tile of the window this wave takes first
   const int m = qg * 32 + col;                  // query vector inside the unit
   const int r_local = m / G;                    // query row inside the tile
   const int head = u.kv_head * G + (m - r_local * G);
@@ -425,27 +424,25 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
     }
   };
 
-  // Issue schedule.  Iterations ("windows", one barrier each) i = 0 ..
-  // groups-1 each consume one group of per_iter tiles: the PV products of
-  // group i and the QK products of group i+1 (one group ahead, so that the QK
-  // MFMAs overlap the softmax VALU work).  Window j issues the V tiles of
-  // group j+lv and then the K tiles of group j+lk, into the ring slots that
-  // window j-1 finished reading.
-  //   per_iter 1 (3-4 q-groups): lk 4, lv 3.  Window i reads K(i+1) and
-  //     V(i); the tiles of windows i-2 and i-1 may still be in flight.
-  //   per_iter 2 (1-2 q-groups, two key streams): lk 2, lv 1; window i reads
-  //     the groups window i-1 issued, so nothing may be in flight.
-  const int groups = (tiles + per_iter - 1) / per_iter;
-  const int lk = kStages / per_iter;
-  const int lv = lk - 1;
-  auto group_tiles = [&](int grp) {
-    return grp < 0 ? 0 : max(0, min(per_iter, tiles - grp * per_iter));
-  };
+  // Issue schedule.  Window i = 0 .. groups-1 consumes tiles 2i and 2i+1:
+  // the PV products of those tiles and the QK products one block ahead, so
+  // that the QK MFMAs overlap the softmax VALU work.  The QK products of
+  // window i read the next group's tiles 2i+2, 2i+3 (two key streams) or
+  // tiles 2i+1, 2i+2 (one stream).  Window j issues V tiles 2j+2, 2j+3 and K
+  // tiles 2j+koff, 2j+koff+1 (koff 4, or 3 for one stream) into the ring
+  // slots that window j-1 finished reading; window i needs everything window
+  // i-1 issued, so nothing is in flight at its barrier.
+  const int groups = (tiles + 1) / 2;
+  const int koff = both ? 3 : 4;
   auto issue = [&](int j) {
-    const int nv = group_tiles(j + lv);
-    for (int k = 0; k < nv; ++k) load_half((j + lv) * per_iter + k, true);
-    const int nk = group_tiles(j + lk);
-    for (int k = 0; k < nk; ++k) load_half((j + lk) * per_iter + k, false);
+    for (int k = 0; k < 2; ++k) {
+      const int t = 2 * j + 2 + k;
+      if (t >= 0 && t < tiles) load_half(t, true);
+    }
+    for (int k = 0; k < 2; ++k) {
+      const int t = 2 * j + koff + k;
+      if (t >= 0 && t < tiles) load_half(t, false);
+    }
   };
   // Wait until at most `newer` half tiles (the newest ones) are in flight.
   auto wait_halves = [&](int newer) {
@@ -454,24 +451,13 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
       case 1: __builtin_amdgcn_s_waitcnt(vmcnt_encoding(DMAS)); break;
       case 2: __builtin_amdgcn_s_waitcnt(vmcnt_encoding(2 * DMAS)); break;
       case 3: __builtin_amdgcn_s_waitcnt(vmcnt_encoding(3 * DMAS)); break;
-      case 4: __builtin_amdgcn_s_waitcnt(vmcnt_encoding(4 * DMAS)); break;
-      case 5: __builtin_amdgcn_s_waitcnt(vmcnt_encoding(5 * DMAS)); break;
-      default: __builtin_amdgcn_s_waitcnt(vmcnt_encoding(6 * DMAS)); break;
+      default: __builtin_amdgcn_s_waitcnt(vmcnt_encoding(4 * DMAS)); break;
     }
-  };
-  // Window i needs V(i) (issued first in window i-lv) and K(i+1) (issued last
-  // in window i+1-lk).  per_iter 1: V(i) is the later one; K(i+2) of window
-  // i-2 and all of window i-1 may still be in flight.  per_iter 2: both come
-  // from window i-1, the latest window, so nothing may be in flight.
-  auto newer_before = [&](int i) {
-    int c = 0;
-    for (int j = i + 2 - lk; j < i; ++j) c += group_tiles(j + lv) + group_tiles(j + lk);
-    return c;
   };
 
   // Lane parts of the LDS read addresses (bytes), including this wave's tile
-  // offset inside its group (my_tile stages) and its block inside the tile;
-  // callers pass the ring stage of the group's first tile.
+  // offset inside its window (my_tile stages); callers pass the ring stage of
+  // the window's first tile.
   const int gq = lane >> 4;
   const int jj = lane & 15;
   const int rr = jj >> 2;
@@ -479,8 +465,7 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
   int k_off[KB];
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb)
-    k_off[kb] = my_tile * STAGEB + (32 * my_blk + col) * ROWB +
-                16 * ((2 * kb + half) ^ swz_k<D>(col));
+    k_off[kb] = my_tile * STAGEB + col * ROWB + 16 * ((2 * kb + half) ^ swz_k<D>(col));
   int v_off[DB][2];
 #pragma unroll
   for (int db = 0; db < DB; ++db)
@@ -488,7 +473,7 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
     for (int hi = 0; hi < 2; ++hi) {
       const int vrow = 16 * half + 4 * hi + rr;
       const int chunk = 4 * db + 2 * (gq & 1) + (cc >> 1);
-      v_off[db][hi] = my_tile * STAGEB + (32 * my_blk + vrow) * ROWB +
+      v_off[db][hi] = my_tile * STAGEB + vrow * ROWB +
                       16 * (chunk ^ swz_v<D>(vrow)) + 8 * (cc & 1);
     }
 
@@ -522,9 +507,9 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
   // kLazyLog2 in exp2 units: until then the probabilities exp2((x - m) * c2)
   // may exceed 1 (at most 2^kLazyLog2, exact in fp32 and as bf16 MFMA
   // operands), and the final division by the sum normalises them all the
-  // same.  With a 32-key block per window the max of one of 32 queries grows
-  // in most windows, so rescaling at every growth would cost 64 multiplies in
-  // most windows.
+  // same.  With 32-key blocks the max of one of 32 queries grows in most
+  // blocks, so rescaling at every growth would cost 64 multiplies in most
+  // blocks.
   auto softmax_max = [&](const float (&x)[16]) {
     float tmax = x[0];
 #pragma unroll
@@ -582,56 +567,55 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
     }
   };
 
-  // Prologue: windows -lk .. -1 of the issue schedule, then QK of group 0,
-  // which needs K(0) from window -lk; everything issued after it may be in
-  // flight: V(0), V(1), K(1), K(2), K(3) (per_iter 1) or V(0), K(1) (per_iter 2).
-  for (int j = -lk; j < 0; ++j) issue(j);
-  {
-    int newer = 0;
-    for (int j = 1 - lk; j < 0; ++j) newer += group_tiles(j + lv) + group_tiles(j + lk);
-    wait_halves(newer);
-  }
+  // Prologue: windows -2 and -1 of the issue schedule, then the first QK
+  // products, which need the K tiles of window -2; V tiles 0, 1 and K tiles
+  // koff-2, koff-1 of window -1 may still be in flight.
+  issue(-2);
+  issue(-1);
+  wait_halves((0 < tiles) + (1 < tiles) + (koff - 2 < tiles) + (koff - 1 < tiles));
   __syncthreads();
   floatx16 s_next;
 #pragma unroll
   for (int r = 0; r < 16; ++r) s_next[r] = 0.0f;
   if (my_tile < tiles) s_next = qk(0);
 
-  auto window = [&](int i) {
-    wait_halves(newer_before(i));
-    __syncthreads();
-    issue(i);
-  };
   // Windows whose issued tiles are all full prefix tiles (i < fast_end) need
-  // none of the schedule arithmetic: the wait count is a constant, the ring
-  // stages are compile-time (K group i+lk lands in group i's stage, V group
-  // i+lk-1 one group earlier) and the sources are one multiply away.
-  const int fast_end = tiles_full / per_iter - lk;
+  // none of the schedule arithmetic: the ring stages are compile-time and the
+  // sources are one multiply away.
+  const int fast_end = (tiles_full - koff) / 2;
   const int64_t tile_bytes = static_cast<int64_t>(kTileKeys) * cstride * 2;
   const uint32_t k_lds_wave = lds_addr(s_k) + wave * DMAS * 1024;
   const uint32_t v_lds_wave = lds_addr(s_v) + wave * DMAS * 1024;
-  auto fast_window = [&](int i, auto per_tag, auto cur_tag, auto stream_tag) {
-    constexpr int PER = decltype(per_tag)::value;  // tiles per window
-    constexpr int kCur = decltype(cur_tag)::value;  // ring stage of group i's first tile
+  auto fast_issue = [&](int i, auto koff_tag, auto cur_tag, auto stream_tag) {
+    constexpr int kK = decltype(koff_tag)::value;
+    constexpr int kCur = decltype(cur_tag)::value;  // ring stage of tile 2i
     constexpr bool kStream = decltype(stream_tag)::value;
-    constexpr int LK = kStages / PER;
-    // per_iter 1: windows i-2 and i-1 each issued one K and one V tile.
-    wait_halves(PER == 1 ? 4 : 0);
-    __syncthreads();
-    const unsigned char* kb = reinterpret_cast<const unsigned char*>(kc) +
-                              static_cast<int64_t>((i + LK) * PER) * tile_bytes;
     const unsigned char* vb = reinterpret_cast<const unsigned char*>(vc) +
-                              static_cast<int64_t>((i + LK - 1) * PER) * tile_bytes;
+                              static_cast<int64_t>(2 * i + 2) * tile_bytes;
+    const unsigned char* kb = reinterpret_cast<const unsigned char*>(kc) +
+                              static_cast<int64_t>(2 * i + kK) * tile_bytes;
 #pragma unroll
-    for (int k = 0; k < PER; ++k) {
+    for (int k = 0; k < 2; ++k) {
 #pragma unroll
       for (int d = 0; d < DMAS; ++d)
         dma16<kStream>(vb + k * tile_bytes, v_dma[d],
-              v_lds_wave + ((kCur + kStages - PER + k) % kStages) * STAGEB + 1024 * d);
+                       v_lds_wave + ((kCur + 2 + k) % kStages) * STAGEB + 1024 * d);
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
 #pragma unroll
       for (int d = 0; d < DMAS; ++d)
         dma16<kStream>(kb + k * tile_bytes, k_dma[d],
-              k_lds_wave + ((kCur + k) % kStages) * STAGEB + 1024 * d);
+                       k_lds_wave + ((kCur + kK + k) % kStages) * STAGEB + 1024 * d);
+    }
+  };
+  auto open_window = [&](int i, auto koff_tag, auto cur_tag, auto stream_tag) {
+    wait_halves(0);
+    __syncthreads();
+    if (i < fast_end) {
+      fast_issue(i, koff_tag, cur_tag, stream_tag);
+    } else {
+      issue(i);
     }
   };
   // Softmax of the current block interleaved with the next block's QK MFMAs;
@@ -652,82 +636,78 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
     pack(x, pf);
   };
 
-  // Steady state: windows whose current and next tiles are full prefix tiles
-  // need no mask, and the ring stages are compile-time constants in loops
-  // unrolled by the ring size.  Every tile of groups i and i+1 is full for
-  // i < steady_end.
-  const int steady_end = max(0, tiles_full / per_iter - 1);
+  // Steady state: windows whose current tiles and the tiles of their QK
+  // products are full prefix tiles need no mask, and the ring stages are
+  // compile-time constants in loops unrolled by two windows (the ring size).
+  // The last tile a window's QK products read is 2i+koff-1.
+  const int steady_end = max(0, (tiles_full - koff + 2) / 2);
   int i = 0;
   bf16x8 pf[2];
-  if (per_iter == 2) {
-    // 1-2 q-groups: at most 64 query vectors, the request's rows fit one row
-    // tile, so the unit is its K/V's only reader.
-    auto step = [&](int w, auto cur_tag, auto next_tag) {
-      if (w < fast_end) {
-        fast_window(w, IntTag<2>{}, cur_tag, BoolTag<true>{});
-      } else {
-        window(w);
-      }
-      softmax_qk(decltype(next_tag)::value, pf);
-      pv(pf, decltype(cur_tag)::value);
-    };
-    for (; i + 2 <= steady_end; i += 2) {
-      step(i, IntTag<0>{}, IntTag<2>{});
-      step(i + 1, IntTag<2>{}, IntTag<0>{});
-    }
-  } else {
+  if (both) {
     auto step = [&](int w, auto cur_tag, auto stream_tag) {
       constexpr int kCur = decltype(cur_tag)::value;
-      if (w < fast_end) {
-        fast_window(w, IntTag<1>{}, cur_tag, stream_tag);
-      } else {
-        window(w);
-      }
-      softmax_qk((kCur + 1) % kStages, pf);
+      open_window(w, IntTag<3>{}, cur_tag, stream_tag);
+      softmax_qk(kCur + 1, pf);
       pv(pf, kCur);
+      softmax_qk((kCur + 2) % kStages, pf);
+      pv(pf, kCur + 1);
     };
     if (stream_kv) {
-      for (; i + 4 <= steady_end; i += 4) {
+      for (; i + 2 <= steady_end; i += 2) {
         step(i, IntTag<0>{}, BoolTag<true>{});
-        step(i + 1, IntTag<1>{}, BoolTag<true>{});
-        step(i + 2, IntTag<2>{}, BoolTag<true>{});
-        step(i + 3, IntTag<3>{}, BoolTag<true>{});
+        step(i + 1, IntTag<2>{}, BoolTag<true>{});
       }
     } else {
-      for (; i + 4 <= steady_end; i += 4) {
+      for (; i + 2 <= steady_end; i += 2) {
         step(i, IntTag<0>{}, BoolTag<false>{});
-        step(i + 1, IntTag<1>{}, BoolTag<false>{});
-        step(i + 2, IntTag<2>{}, BoolTag<false>{});
-        step(i + 3, IntTag<3>{}, BoolTag<false>{});
+        step(i + 1, IntTag<2>{}, BoolTag<false>{});
       }
+    }
+  } else {
+    // 1-2 q-groups: at most 64 query vectors, the request's rows fit one row
+    // tile, so the unit is its K/V's only reader.
+    auto step = [&](int w, auto cur_tag) {
+      constexpr int kCur = decltype(cur_tag)::value;
+      open_window(w, IntTag<4>{}, cur_tag, BoolTag<true>{});
+      softmax_qk((kCur + 2) % kStages, pf);
+      pv(pf, kCur);
+    };
+    for (; i + 2 <= steady_end; i += 2) {
+      step(i, IntTag<0>{});
+      step(i + 1, IntTag<2>{});
     }
   }
   // Remaining windows: runtime stages, masks from the key limit and the
   // ancestor bitsets.
   for (; i < groups; ++i) {
-    window(i);
-    const int t = i * per_iter + my_tile;
-    const int t_next = t + per_iter;
-    float x[16];
+    wait_halves(0);
+    __syncthreads();
+    issue(i);
+    for (int b = 0; b < (both ? 2 : 1); ++b) {
+      const int t = 2 * i + my_tile + b;
+      const int t_next = both ? t + 1 : t + 2;
+      float x[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) x[r] = s_next[r];
-    if (t_next < tiles) s_next = qk(((i + 1) * per_iter) % kStages);
-    if (t < tiles) {
-      const bool tree = t >= tiles_prefix;
-      const int key0 = (tree ? t - tiles_prefix : t) * kTileKeys + 32 * my_blk;
-      const int limit = tree ? n : prefix_keys;
-      const uint32_t bits = tree ? (s_anc[r_local][key0 >> 5] >> (16 * half)) : 0xffffffffu;
-      const int first = key0 + 16 * half;
+      for (int r = 0; r < 16; ++r) x[r] = s_next[r];
+      if (t_next < tiles) s_next = qk((t_next - my_tile) % kStages);
+      if (t < tiles) {
+        const bool tree = t >= tiles_prefix;
+        const int key0 = (tree ? t - tiles_prefix : t) * kTileKeys;
+        const int limit = tree ? n : prefix_keys;
+        const uint32_t bits = tree ? (s_anc[r_local][key0 >> 5] >> (16 * half)) : 0xffffffffu;
+        const int first = key0 + 16 * half;
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        x[r] = (first + r < limit && ((bits >> r) & 1u)) ? x[r] : -__builtin_inff();
-      softmax_max(x);
-      softmax_exp(x);
-      pack(x, pf);
-      pv(pf, (i * per_iter) % kStages);
+        for (int r = 0; r < 16; ++r)
+          x[r] = (first + r < limit && ((bits >> r) & 1u)) ? x[r] : -__builtin_inff();
+        softmax_max(x);
+        softmax_exp(x);
+        pack(x, pf);
+        pv(pf, (t - my_tile) % kStages);
+      }
     }
   }
   __syncthreads();
+
 
   // Merge the key streams of each q-group through LDS (the ring is free now).
   // Slot k (k = (ks-1)*nq + qg < 6) lives at float offset k*STATE*64 of s_k|s_v.
