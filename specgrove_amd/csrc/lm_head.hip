@@ -15,7 +15,11 @@
 //               128 x 128 quarter (tokens 128*(w&1).., rows 128*(w>>1)..);
 //   ring      = four stages of 32 hidden dims: the weight and hidden chunks
 //               move HBM -> LDS with global_load_lds_dwordx4 (no register
-//               staging), three stages ahead of the MFMAs;
+//               staging), 64 contiguous bytes of each row per copy lane
+//               group, three stages ahead of the MFMAs; a stage's copies,
+//               its fragment reads for the next stage and its MFMAs are
+//               interleaved in four parts, so that the four waves' LDS
+//               traffic does not queue up right after the barrier;
 //   product   = C^T = W X^T with v_mfma_f32_32x32x16_bf16 (A = weight rows, B =
 //               hidden rows), so each lane ends with 64 logits of one row per
 //               32-row block, fp32-accumulated over the hidden dims in
@@ -57,7 +61,6 @@ constexpr int kTileV = 256;          // vocabulary tokens per workgroup tile
 constexpr int kStepK = 32;           // hidden dims per ring stage
 constexpr int kLmStages = 4;
 constexpr int kWBytes = kTileV * kStepK * 2;  // weight bytes per stage (16 KiB)
-constexpr int kWKb = kWBytes / 2;             // one 16-dim block of the weight stage
 constexpr int kStatTokens = 128;     // tokens per statistics tile
 constexpr int kOutPitch = 2 * 128 + 16;  // LDS staging row: 128 bf16 + 16 bytes
 constexpr int kLmXcds = 8;
@@ -70,7 +73,6 @@ template <int R>
 struct RowTile {
   static constexpr int kRows = 64 * R;
   static constexpr int kXBytes = kRows * kStepK * 2;   // hidden bytes per stage
-  static constexpr int kXKb = kXBytes / 2;
   static constexpr int kStage = kWBytes + kXBytes;
   static constexpr int kDmas = 4 + R;                  // copies per wave per stage
   static constexpr int kStaging = 4 * 32 * R * kOutPitch;
@@ -143,35 +145,38 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
   const int r0 = rt * T::kRows;
 
   // DMA slots.  Per stage the weight is 16 copies of 1 KiB (wave w issues
-  // 4w .. 4w+3) and the hidden rows 4R (wave w issues Rw .. Rw+R-1).  Copy q
-  // of an operand covers 16-dim block q / (rows/32) and 32-row block
-  // q % (rows/32); lane i moves row 32*(q % (rows/32)) + i%32, dims 8*(i/32)
-  // .. +7 of that block.  LDS layout of an operand stage: [16-dim block]
-  // [32-row block][8-dim half][32 rows][8 dims], which is the MFMA operand
-  // layout itself: lane l's fragment of a 32-row block is the 16 bytes at
-  // 16*l, so every fragment read is one linear 1 KiB (no bank conflicts).
+  // 4w .. 4w+3) and the hidden rows 4R (wave w issues Rw .. Rw+R-1).  LDS
+  // layout of an operand stage: rows of 64 bytes (the stage's 32 dims) whose
+  // 16-byte chunk c sits at chunk c ^ swz(row), swz(row) = (row >> 1) & 3, so
+  // that a fragment read (32 rows, one chunk each, eight lanes per LDS cycle)
+  // touches eight distinct bank groups.  A copy lane reads 16 contiguous
+  // bytes and four lanes one row's 64 bytes: every copy touches 16 cache
+  // lines instead of 32.
   uint32_t w_off[4], w_lds[4], x_off[R], x_lds[R];
   const unsigned char* wbase =
       static_cast<const unsigned char*>(a.weight_dev) + static_cast<int64_t>(v0) * a.weight_row_stride * 2;
   const unsigned char* xbase = static_cast<const unsigned char*>(a.hidden_dev);
   bool bad_index = false;
+  // Copy q moves rows 16q .. 16q+15 of an operand, 64 bytes (the stage's 32
+  // dims) of each: lane i reads row 16q + i/4, 16-byte chunk (i%4) ^ swz(row),
+  // and lands at LDS chunk i%4 of that row.
+  const int g_lane = (lane & 3) ^ ((lane >> 3) & 3);  // swz(row) = (row >> 1) & 3
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int q = wave * 4 + i;
-    const int row = 32 * (q & 7) + (lane & 31);
-    const int dim = 16 * (q >> 3) + 8 * (lane >> 5);
+    const int row = 16 * q + (lane >> 2);
+    const int dim = 8 * g_lane;
     // Tokens past the vocabulary re-read the last token (finite data the
     // epilogue drops).
     const int tok = min(v0 + row, V - 1) - v0;
     w_off[i] = static_cast<uint32_t>((static_cast<int64_t>(tok) * a.weight_row_stride + dim) * 2);
-    w_lds[i] = static_cast<uint32_t>((q >> 3) * kWKb + 1024 * (q & 7));
+    w_lds[i] = static_cast<uint32_t>(1024 * q);
   }
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     const int q = wave * R + i;
-    const int blocks = 2 * R;  // 32-row blocks of the row tile
-    const int row = 32 * (q % blocks) + (lane & 31);
-    const int dim = 16 * (q / blocks) + 8 * (lane >> 5);
+    const int row = 16 * q + (lane >> 2);
+    const int dim = 8 * g_lane;
     // Rows past the projected rows re-read a valid row.
     const int prow = min(r0 + row, a.num_rows - 1);
     int src = a.row_index_dev != nullptr ? a.row_index_dev[prow] : prow;
@@ -180,7 +185,7 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
       src = 0;
     }
     x_off[i] = static_cast<uint32_t>((static_cast<int64_t>(src) * a.hidden_row_stride + dim) * 2);
-    x_lds[i] = static_cast<uint32_t>(kWBytes + (q / blocks) * T::kXKb + 1024 * (q % blocks));
+    x_lds[i] = static_cast<uint32_t>(kWBytes + 1024 * q);
   }
   if (bad_index && a.status_dev != nullptr) atomicExch(a.status_dev, SG_EINVAL);
 
@@ -206,8 +211,14 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
 
   const int wv = wave & 1;   // vocabulary half of the tile
   const int wr = wave >> 1;  // row half of the tile
-  const int a_lane = wv * 4 * 1024 + 16 * lane;  // first of this wave's 32-row blocks
-  const int b_lane = wr * R * 1024 + 16 * lane;
+  // Fragment (kb, 32-row block) of lane l: row l%32 of the block, chunk
+  // 2kb + l/32, stored at LDS chunk (2kb + l/32) ^ swz(l%32) of the 64-byte row.
+  int lp[2];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+    lp[kb] = (lane & 31) * 64 + 16 * ((2 * kb + (lane >> 5)) ^ (((lane & 31) >> 1) & 3));
+  const int a_base = wv * 4 * 2048;  // first of this wave's 32-row blocks
+  const int b_base = kWBytes + wr * R * 2048;
 
   // Operand fragments of one stage: weight rows (A) and hidden rows (B) of
   // both 16-dim blocks, read from LDS one stage ahead of their MFMAs.
@@ -222,11 +233,11 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
 #pragma unroll
       for (int vb = 0; vb < 4; ++vb)
         f.w[kb][vb] =
-            as_bf16x8(*reinterpret_cast<const uint4*>(st + kb * kWKb + a_lane + vb * 1024));
+            as_bf16x8(*reinterpret_cast<const uint4*>(st + a_base + vb * 2048 + lp[kb]));
 #pragma unroll
       for (int rb = 0; rb < R; ++rb)
-        f.x[kb][rb] = as_bf16x8(*reinterpret_cast<const uint4*>(
-            st + kWBytes + kb * T::kXKb + b_lane + rb * 1024));
+        f.x[kb][rb] =
+            as_bf16x8(*reinterpret_cast<const uint4*>(st + b_base + rb * 2048 + lp[kb]));
     }
   };
   auto mma = [&](const Frags& f) {
@@ -239,10 +250,11 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
           acc[vb][rb] =
               __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.w[kb][vb], f.x[kb][rb], acc[vb][rb], 0, 0, 0);
   };
+  for (int s = 0; s < kLmStages - 1 && s < steps; ++s) issue(s);
   // Stage s: wait for its copies (only the up to two later stages' remain in
-  // flight), publish it with the barrier (which also ends every wave's reads
-  // of stage s-1), refill stage s-1's slot with stage s+3.
-  auto open_stage = [&](int s) {
+  // flight) and publish it with the barrier, which also ends every wave's
+  // reads of stage s-1.
+  auto wait_stage = [&](int s) {
     const int newer = min(kLmStages - 2, steps - 1 - s);
     if (newer >= 2) {
       __builtin_amdgcn_s_waitcnt(vmcnt_encoding(2 * T::kDmas));
@@ -252,26 +264,76 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
       __builtin_amdgcn_s_waitcnt(vmcnt_encoding(0));
     }
     __syncthreads();
-    if (s + kLmStages - 1 < steps) issue(s + kLmStages - 1);
   };
-
-  for (int s = 0; s < kLmStages - 1 && s < steps; ++s) issue(s);
-  // Software pipeline: the fragments of stage s are read while the MFMAs of
-  // stage s-1 run.
-  // steps is even (hidden_size % 64 == 0): stage 0, pairs of stages, and a
-  // final stage, with no data-dependent branch around the accumulators.
+  // Stage s in four parts p (one 32-row weight block each): the MFMAs of
+  // stage s-1's dims (fragments `cur`, read during stage s-1), a quarter of
+  // the fragment reads of stage s (into `next`) placed one after each of the
+  // part's first MFMAs, and a quarter of the copies that refill stage s-1's
+  // slot with stage s+3.
+  auto run_stage = [&](int s, Frags& next, const Frags& cur) {
+    wait_stage(s);
+    const bool refill = s + kLmStages - 1 < steps;
+    const int t = s + kLmStages - 1;
+    const uint32_t stage_t = ring + (t % kLmStages) * T::kStage;
+    const unsigned char* wk = wbase + static_cast<int64_t>(t) * kStepK * 2;
+    const unsigned char* xk = xbase + static_cast<int64_t>(t) * kStepK * 2;
+    const unsigned char* st = smem + (s % kLmStages) * T::kStage;
+    constexpr int nd = 4 + R;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        next.w[kb][p] =
+            as_bf16x8(*reinterpret_cast<const uint4*>(st + a_base + p * 2048 + lp[kb]));
+        if (p < R)
+          next.x[kb][p] =
+              as_bf16x8(*reinterpret_cast<const uint4*>(st + b_base + p * 2048 + lp[kb]));
+      }
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int rb = 0; rb < R; ++rb)
+          acc[p][rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur.w[kb][p], cur.x[kb][rb],
+                                                               acc[p][rb], 0, 0, 0);
+      if (p < R) {
+        constexpr int kPairs = 4 < 2 * R ? 4 : 2 * R;
+#pragma unroll
+        for (int k = 0; k < kPairs; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        if constexpr (2 * R > kPairs) __builtin_amdgcn_sched_group_barrier(0x008, 2 * R - kPairs, 0);
+        if constexpr (4 > kPairs) __builtin_amdgcn_sched_group_barrier(0x100, 4 - kPairs, 0);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        if constexpr (2 * R > 2) __builtin_amdgcn_sched_group_barrier(0x008, 2 * R - 2, 0);
+      }
+      if (refill) {
+#pragma unroll
+        for (int d = p * nd / 4; d < (p + 1) * nd / 4; ++d) {
+          if (d < 4) {
+            dma16(wk, w_off[d], stage_t + w_lds[d]);
+          } else {
+            dma16(xk, x_off[d - 4], stage_t + x_lds[d - 4]);
+          }
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
   Frags f0, f1;
-  open_stage(0);
+  wait_stage(0);
+  if (kLmStages - 1 < steps) issue(kLmStages - 1);
   load_frags(0, f0);
   for (int s = 1; s + 1 < steps; s += 2) {
-    open_stage(s);
-    load_frags(s, f1);
-    mma(f0);
-    open_stage(s + 1);
-    load_frags(s + 1, f0);
-    mma(f1);
+    run_stage(s, f1, f0);
+    run_stage(s + 1, f0, f1);
   }
-  open_stage(steps - 1);
+  wait_stage(steps - 1);
   load_frags(steps - 1, f1);
   mma(f0);
   mma(f1);
