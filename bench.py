@@ -174,15 +174,49 @@ def attention_call(ops, wl, plan, meta, st):
                        out=st["out"])
 
 
-def commit_call(ops, wl, meta, st):
+def commit_args(wl, meta, st):
     kc = st["kc"]
     kt = st["kt"]
-    ops.kv_commit(*st["ptrs"], num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim,
-                  cache_head_stride=kc.stride(0), cache_token_stride=kc.stride(1),
-                  tree_row_stride=kt.stride(0), tree_head_stride=kt.stride(1),
-                  row_offset=meta["row_offset"], keep_rows=meta["keep_rows"],
-                  keep_len=meta["keep_len"], prefix_start=meta["prefix_start"],
-                  lengths=st["lengths"], capacity=wl.capacity)
+    return dict(num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim,
+                cache_head_stride=kc.stride(0), cache_token_stride=kc.stride(1),
+                tree_row_stride=kt.stride(0), tree_head_stride=kt.stride(1),
+                row_offset=meta["row_offset"], keep_rows=meta["keep_rows"],
+                keep_len=meta["keep_len"], prefix_start=meta["prefix_start"],
+                lengths=st["lengths"], capacity=wl.capacity)
+
+
+def commit_call(ops, wl, meta, st):
+    ops.kv_commit(*st["ptrs"], **commit_args(wl, meta, st))
+
+
+def host_costs(torch, ops, wl, plan, meta, sets, iters):
+    """Host microseconds per call (enqueue only; the GPU runs behind) of the
+    checked entry points and of the same calls prepared once (argument checks
+    and struct built outside the loop), plus the prepared one-layer commit
+    timed back to back on the GPU."""
+    def host_us(fn):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for k in range(iters):
+            fn(k)
+        us = (time.perf_counter() - t0) / iters * 1e6
+        torch.cuda.synchronize()
+        return us
+    attn = [ops.prepare_tree_attention(st["q"], st["kc"], st["vc"], st["kt"], st["vt"],
+                                       meta["row_offset"], meta["prefix_start"],
+                                       meta["prefix_len"], meta["parent"], plan, out=st["out"])
+            for st in sets]
+    commit = [ops.prepare_kv_commit(*st["ptrs"], **commit_args(wl, meta, st)) for st in sets]
+    n = len(sets)
+    out = {
+        "tree_attention_us": host_us(lambda k: attention_call(ops, wl, plan, meta, sets[k % n])),
+        "tree_attention_prepared_us": host_us(lambda k: attn[k % n]()),
+        "kv_commit_us": host_us(lambda k: commit_call(ops, wl, meta, sets[k % n])),
+        "kv_commit_prepared_us": host_us(lambda k: commit[k % n]()),
+    }
+    out["kv_commit_prepared_gpu_us_back_to_back"] = back_to_back(
+        torch, lambda k: commit[k % n](), iters) * 1e3
+    return out
 
 
 def commit_all_layers(torch, np, ops, wl, meta, device, layers=36, iters=50, warmup=5):
@@ -681,7 +715,8 @@ def main():
             "gbs": wl.commit_bytes() / (commit_b2b * 1e-3) / 1e9,
             "all_layers": commit_all_layers(torch, np, ops, wl, meta, device),
         },
-        "host": {"us_per_step_enqueue": host_us},
+        "host": dict(us_per_step_enqueue=host_us,
+                     **host_costs(torch, ops, wl, plan, meta, sets, steps)),
     }
     del sets
     torch.cuda.empty_cache()
