@@ -147,9 +147,10 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
   // DMA slots.  Per stage the weight is 16 copies of 1 KiB (wave w issues
   // 4w .. 4w+3) and the hidden rows 4R (wave w issues Rw .. Rw+R-1).  LDS
   // layout of an operand stage: rows of 64 bytes (the stage's 32 dims) whose
-  // 16-byte chunk c sits at chunk c ^ swz(row), swz(row) = (row >> 1) & 3, so
-  // that a fragment read (32 rows, one chunk each, eight lanes per LDS cycle)
-  // touches eight distinct bank groups.  A copy lane reads 16 contiguous
+  // 16-byte chunk c sits at chunk c ^ swz(row), swz(row) = (row >> 2) & 3, so
+  // that each group of 16 lanes of a fragment read (16 consecutive rows, one
+  // chunk each; one 256-byte LDS cycle) touches 16 distinct 16-byte bank
+  // groups.  A copy lane reads 16 contiguous
   // bytes and four lanes one row's 64 bytes: every copy touches 16 cache
   // lines instead of 32.
   uint32_t w_off[4], w_lds[4], x_off[R], x_lds[R];
@@ -160,7 +161,7 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
   // Copy q moves rows 16q .. 16q+15 of an operand, 64 bytes (the stage's 32
   // dims) of each: lane i reads row 16q + i/4, 16-byte chunk (i%4) ^ swz(row),
   // and lands at LDS chunk i%4 of that row.
-  const int g_lane = (lane & 3) ^ ((lane >> 3) & 3);  // swz(row) = (row >> 1) & 3
+  const int g_lane = (lane & 3) ^ ((lane >> 4) & 3);  // swz(row) = (row >> 2) & 3
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int q = wave * 4 + i;
@@ -216,7 +217,7 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
   int lp[2];
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
-    lp[kb] = (lane & 31) * 64 + 16 * ((2 * kb + (lane >> 5)) ^ (((lane & 31) >> 1) & 3));
+    lp[kb] = (lane & 31) * 64 + 16 * ((2 * kb + (lane >> 5)) ^ (((lane & 31) >> 2) & 3));
   const int a_base = wv * 4 * 2048;  // first of this wave's 32-row blocks
   const int b_base = kWBytes + wr * R * 2048;
 
