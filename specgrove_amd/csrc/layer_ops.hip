@@ -114,10 +114,14 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(
   }
 }
 
-// One row per workgroup, one head per wave at a time; lane l holds dims l and
-// l + D/2 (a rotary pair).  Heads 0..Hq-1 are q (normed, rotated, written to
-// q_out[row, h]), Hq..Hq+Hkv-1 are k (normed, rotated, written to
-// k_out[h, row]), the rest v (copied to v_out[h, row]).
+// One row per workgroup.  A head's D dims are D/8 lanes of 16 bytes (lane j
+// holds dims 8j .. 8j+7), so a wave takes 64/(D/8) heads at a time with
+// 16-byte loads and stores; the rotary partner of dim i < D/2 (dim i + D/2)
+// sits in lane j ^ (D/16) of the same head.  Heads 0..Hq-1 are q (normed,
+// rotated, written to q_out[row, h]), Hq..Hq+Hkv-1 are k (normed, rotated,
+// written to k_out[h, row]), the rest v (copied to v_out[h, row]).  The
+// row's bf16 cos / sin of the fp32 angles position * inv_freq[p] are made once
+// per workgroup (one pair per thread) and read from LDS.
 template <int D>
 __global__ __launch_bounds__(kNormThreads) void qk_norm_rope_kernel(
     const uint16_t* __restrict__ qkv, int64_t qkv_stride, int hq, int hkv,
@@ -126,61 +130,90 @@ __global__ __launch_bounds__(kNormThreads) void qk_norm_rope_kernel(
     uint16_t* __restrict__ q_out, int64_t q_row_stride, uint16_t* __restrict__ k_out,
     uint16_t* __restrict__ v_out, int64_t kv_head_stride, float eps) {
   constexpr int H2 = D / 2;
-  constexpr int PER = H2 >= 64 ? H2 / 64 : 1;  // rotary pairs per lane
-  static_assert(H2 % 64 == 0 || H2 < 64, "head_dim");
+  constexpr int LPH = D / 8;        // lanes per head
+  constexpr int HPW = kWave / LPH;  // heads per wave at a time
+  __shared__ float s_cs[H2];
+  __shared__ float s_sn[H2];
   const int64_t row = blockIdx.x;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int waves = blockDim.x >> 6;
   const float pos = static_cast<float>(positions[row]);
-  const bool active = lane < H2;  // D = 64: lanes 32..63 hold no pair
-  float cs[PER], sn[PER];
-#pragma unroll
-  for (int p = 0; p < PER; ++p) {
-    const float ang = active ? pos * inv_freq[lane + 64 * p] : 0.0f;
+  for (int p = threadIdx.x; p < H2; p += blockDim.x) {
     float sv, cv;
-    sincosf(ang, &sv, &cv);
-    cs[p] = bf16r(cv);
-    sn[p] = bf16r(sv);
+    sincosf(pos * inv_freq[p], &sv, &cv);
+    s_cs[p] = bf16r(cv);
+    s_sn[p] = bf16r(sv);
+  }
+  __syncthreads();
+  const int j = lane % LPH;             // 16-byte chunk of the head
+  const int slot = lane / LPH;          // head of the wave's group
+  const bool lower = j < LPH / 2;       // dims below D/2
+  const int pair0 = 8 * (j % (LPH / 2));
+  float cs[8], sn[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    cs[k] = s_cs[pair0 + k];
+    sn[k] = s_sn[pair0 + k];
   }
   const int heads = hq + 2 * hkv;
-  for (int h = wave; h < heads; h += waves) {
-    const uint16_t* src = qkv + row * qkv_stride + static_cast<int64_t>(h) * D;
-    float a[PER], b[PER];
+  for (int h0 = wave * HPW; h0 < heads; h0 += waves * HPW) {
+    const int h = h0 + slot;
+    const bool live = h < heads;
+    const bool is_v = h >= hq + hkv;
+    const uint16_t* src = qkv + row * qkv_stride + static_cast<int64_t>(h) * D + 8 * j;
+    const uint4 raw = live ? *reinterpret_cast<const uint4*>(src) : make_uint4(0u, 0u, 0u, 0u);
+    const uint32_t rv[4] = {raw.x, raw.y, raw.z, raw.w};
+    float x[8];
 #pragma unroll
-    for (int p = 0; p < PER; ++p) {
-      a[p] = active ? bf16_to_f32(src[lane + 64 * p]) : 0.0f;
-      b[p] = active ? bf16_to_f32(src[lane + 64 * p + H2]) : 0.0f;
+    for (int k = 0; k < 4; ++k) {
+      x[2 * k] = bf16_to_f32(rv[k] & 0xffffu);
+      x[2 * k + 1] = bf16_to_f32(rv[k] >> 16);
     }
-    if (h >= hq + hkv) {  // v: copy
-      uint16_t* dst = v_out + static_cast<int64_t>(h - hq - hkv) * kv_head_stride + row * D;
-      if (active) {
-#pragma unroll
-        for (int p = 0; p < PER; ++p) {
-          dst[lane + 64 * p] = src[lane + 64 * p];
-          dst[lane + 64 * p + H2] = src[lane + 64 * p + H2];
-        }
-      }
-      continue;
-    }
+    // RMS over the head's D dims: the lane's 8 squares, then the head's lanes.
     float ss = 0.0f;
 #pragma unroll
-    for (int p = 0; p < PER; ++p) ss += a[p] * a[p] + b[p] * b[p];
+    for (int k = 0; k < 8; ++k) ss += x[k] * x[k];
 #pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) ss += __shfl_xor(ss, d);
+    for (int d = LPH / 2; d >= 1; d >>= 1) ss += __shfl_xor(ss, d);
     const float r = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
-    const uint16_t* w = h < hq ? q_norm : k_norm;
-    uint16_t* dst = h < hq ? q_out + row * q_row_stride + static_cast<int64_t>(h) * D
-                           : k_out + static_cast<int64_t>(h - hq) * kv_head_stride + row * D;
-    if (!active) continue;
+    const uint16_t* w = (h < hq ? q_norm : k_norm) + 8 * j;
+    const uint4 wraw = (live && !is_v) ? *reinterpret_cast<const uint4*>(w)
+                                       : make_uint4(0u, 0u, 0u, 0u);
+    const uint32_t wv[4] = {wraw.x, wraw.y, wraw.z, wraw.w};
+    uint32_t nx[4];
 #pragma unroll
-    for (int p = 0; p < PER; ++p) {
-      const int i = lane + 64 * p;
-      const float na = bf16r(bf16_to_f32(w[i]) * bf16r(a[p] * r));
-      const float nb = bf16r(bf16_to_f32(w[i + H2]) * bf16r(b[p] * r));
-      // x*cos + rotate_half(x)*sin, rotate_half(x) = (-x2, x1).
-      dst[i] = f32_to_bf16(na * cs[p] - nb * sn[p]);
-      dst[i + H2] = f32_to_bf16(nb * cs[p] + na * sn[p]);
+    for (int k = 0; k < 4; ++k) {
+      const float lo = bf16_to_f32(wv[k] & 0xffffu) * bf16r(x[2 * k] * r);
+      const float hi = bf16_to_f32(wv[k] >> 16) * bf16r(x[2 * k + 1] * r);
+      nx[k] = pack_bf16x2(lo, hi);
+    }
+    // The rotary partner's normed values (exact: bf16 pairs).
+    uint32_t ny[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) ny[k] = __shfl_xor(nx[k], LPH / 2);
+    uint32_t o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float e[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const float a = bf16_to_f32(t ? (nx[k] >> 16) : (nx[k] & 0xffffu));
+        const float b = bf16_to_f32(t ? (ny[k] >> 16) : (ny[k] & 0xffffu));
+        const int q = 2 * k + t;
+        // x*cos + rotate_half(x)*sin, rotate_half(x) = (-x2, x1).
+        e[t] = lower ? a * cs[q] - b * sn[q] : a * cs[q] + b * sn[q];
+      }
+      o[k] = pack_bf16x2(e[0], e[1]);
+    }
+    if (!live) continue;
+    if (is_v) {
+      *reinterpret_cast<uint4*>(v_out + static_cast<int64_t>(h - hq - hkv) * kv_head_stride +
+                                row * D + 8 * j) = raw;
+    } else {
+      uint16_t* dst = h < hq ? q_out + row * q_row_stride + static_cast<int64_t>(h) * D
+                             : k_out + static_cast<int64_t>(h - hq) * kv_head_stride + row * D;
+      *reinterpret_cast<uint4*>(dst + 8 * j) = make_uint4(o[0], o[1], o[2], o[3]);
     }
   }
 }
@@ -292,6 +325,11 @@ extern "C" int sg_qk_norm_rope(const SgQkNormRopeArgs* args, sg_stream_t stream)
              "q row stride below Hq*D");
   SG_REQUIRE(a.kv_head_stride >= static_cast<int64_t>(a.num_rows) * a.head_dim,
              "k/v head stride below R*D");
+  SG_REQUIRE((a.qkv_row_stride | a.q_row_stride | a.kv_head_stride) % 8 == 0,
+             "row and head strides must be multiples of 8 elements");
+  SG_REQUIRE(aligned16(a.qkv_dev) && aligned16(a.q_norm_dev) && aligned16(a.k_norm_dev) &&
+                 aligned16(a.q_out_dev) && aligned16(a.k_out_dev) && aligned16(a.v_out_dev),
+             "q/k/v, norm weights and outputs must be 16-byte aligned");
   hipStream_t s = static_cast<hipStream_t>(stream);
   auto go = [&](auto kernel) {
     kernel<<<dim3(a.num_rows), dim3(kNormThreads), 0, s>>>(

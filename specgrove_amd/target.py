@@ -42,7 +42,7 @@ from . import _lib, attention, ops
 
 
 def _stream():
-    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    return ctypes.c_void_p(ops._stream_handle())
 
 
 def add_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
