@@ -408,6 +408,47 @@ def lm_head_bench(torch, np, W, ops, device, iters=10, warmup=2):
             line["library_gemm_us"] = gemm * 1e3
             line["library_gemm_plus_stats_us"] = (gemm + stats) * 1e3
         out[name] = line
+    out["verify_wave"] = verify_wave_bench(torch, np, W, ops, wl, hidden, weight, device)
+    return out
+
+
+def verify_wave_bench(torch, np, W, ops, wl, hidden, weight, device, iters=5):
+    """Wall time per wave of the whole verification from the final hidden
+    rows (host transfers between the passes included): the lazy projection
+    (internal rows, walks, reached leaves, leaf draws), projecting every row
+    with the fused head then the tree verifier on its bf16 logits, and the
+    library GEMM then the same verifier.  Every variant draws each request's
+    uniforms from its own generator, as the reference does."""
+    from specgrove_amd import verify
+    vocab = weight.shape[0]
+    tokens = [[int(t) % vocab for t in ts] for ts in wl.tokens]
+    count = wl.num_requests
+    generators = [torch.Generator(device=device).manual_seed(500 + i) for i in range(count)]
+
+    def lazy():
+        verify.tree_verify_hip_lazy_projection_batched(wl.parents, tokens, hidden, weight,
+                                                       generators=generators)
+
+    def fused_full():
+        logits = ops.lm_head(hidden, weight).logits[:, :vocab]
+        verify.tree_verify_hip_rejection_batched(wl.parents, tokens, logits,
+                                                 generators=generators)
+
+    def library_full():
+        logits = torch.matmul(hidden, weight.T)
+        verify.tree_verify_hip_rejection_batched(wl.parents, tokens, logits,
+                                                 generators=generators)
+
+    out = {"requests": count, "rows": wl.total_rows}
+    for name, fn in (("lazy_projection_us", lazy), ("every_row_fused_head_us", fused_full),
+                     ("every_row_library_gemm_us", library_full)):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            fn()
+        torch.cuda.synchronize()
+        out[name] = (time.perf_counter() - t0) / iters * 1e6
     return out
 
 

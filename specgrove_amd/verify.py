@@ -51,6 +51,19 @@ def _topology(parents, tokens):
     return parents, tokens, max(depths)
 
 
+def _draw_uniforms(topologies, generators, device):
+    """Each request's 2*(depth+1) fp32 uniforms from its own generator (the
+    reference's per-request draw), written straight into its row of one
+    [n, 2*(max_depth+1)] tensor; returns (uniforms, max_depth)."""
+    max_depth = max(depth for _, _, depth in topologies)
+    uniforms = torch.zeros((len(topologies), 2 * (max_depth + 1)), dtype=torch.float32,
+                           device=device)
+    for i, ((_, _, depth), generator) in enumerate(zip(topologies, generators)):
+        torch.rand(2 * (depth + 1), dtype=torch.float32, device=device, generator=generator,
+                   out=uniforms[i, :2 * (depth + 1)])
+    return uniforms, max_depth
+
+
 def tree_verify_hip_rejection_batched(parents_batch: Sequence[Sequence[int]],
                                       tokens_batch: Sequence[Sequence[int]],
                                       all_logits: torch.Tensor, temperature: float = 1.0,
@@ -101,12 +114,7 @@ def tree_verify_hip_rejection_batched(parents_batch: Sequence[Sequence[int]],
         raise FloatingPointError("Invalid Target logits for the HIP tree verifier")
 
     device = logits.device
-    max_depth = max(depth for _, _, depth in topologies)
-    stride = 2 * (max_depth + 1)
-    uniforms = torch.zeros((count, stride), dtype=torch.float32, device=device)
-    for i, ((_, _, depth), generator) in enumerate(zip(topologies, generators)):
-        uniforms[i, :2 * (depth + 1)] = torch.rand(2 * (depth + 1), dtype=torch.float32,
-                                                   device=device, generator=generator)
+    uniforms, max_depth = _draw_uniforms(topologies, generators, device)
     row_offset = np.zeros(count + 1, np.int32)
     np.cumsum(rows, out=row_offset[1:])
     parent = np.concatenate([np.asarray(p, np.int32) for p, _, _ in topologies])
@@ -234,12 +242,7 @@ def tree_verify_hip_lazy_projection_batched(parents_batch: Sequence[Sequence[int
     meta_row_map = meta[n1 + 2 * total:n1 + 3 * total]
     meta_internal = meta[n1 + 3 * total:]
 
-    max_depth = max(depth for _, _, depth in topologies)
-    stride = 2 * (max_depth + 1)
-    uniforms = torch.zeros((count, stride), dtype=torch.float32, device=device)
-    for i, ((_, _, depth), generator) in enumerate(zip(topologies, generators)):
-        uniforms[i, :2 * (depth + 1)] = torch.rand(2 * (depth + 1), dtype=torch.float32,
-                                                   device=device, generator=generator)
+    uniforms, max_depth = _draw_uniforms(topologies, generators, device)
 
     def projection_valid(head: "ops.LmHeadResult") -> torch.Tensor:
         ok = (torch.isfinite(head.row_max).all() & torch.isfinite(head.row_sum).all()
