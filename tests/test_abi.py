@@ -233,6 +233,31 @@ def test_lm_head_and_projected_sampler_reject_bad_arguments_on_the_host():
     assert lib.sg_tree_sample(ctypes.byref(s), None) == _lib.SG_EINVAL
 
 
+def test_layer_ops_reject_bad_arguments_on_the_host():
+    """The decoder-stack kernels check shapes, strides and 16-byte alignment
+    before any launch (fake, never-dereferenced device addresses)."""
+    lib = _lib.load()
+    a = _lib.SgQkNormRopeArgs()
+    a.num_rows, a.num_q_heads, a.num_kv_heads, a.head_dim, a.eps = 4, 32, 8, 128, 1e-6
+    for name in ("qkv_dev", "q_norm_dev", "k_norm_dev", "inv_freq_dev", "positions_dev",
+                 "q_out_dev", "k_out_dev", "v_out_dev"):
+        setattr(a, name, 0x1000)
+    a.qkv_row_stride, a.q_row_stride, a.kv_head_stride = 48 * 128, 32 * 128, 4 * 128
+    for field, value, text in (("head_dim", 96, b"head_dim"),
+                               ("qkv_row_stride", 40 * 128, b"qkv row stride"),
+                               ("kv_head_stride", 3 * 128, b"head stride"),
+                               ("q_row_stride", 32 * 128 + 4, b"multiples of 8"),
+                               ("q_out_dev", 0x1008, b"aligned"),
+                               ("k_norm_dev", 0x1004, b"aligned")):
+        good = getattr(a, field)
+        setattr(a, field, value)
+        assert lib.sg_qk_norm_rope(ctypes.byref(a), None) == _lib.SG_EINVAL, field
+        assert text in lib.sg_last_error(), (field, lib.sg_last_error())
+        setattr(a, field, good)
+    a.num_rows = 0  # nothing to do: no launch
+    assert lib.sg_qk_norm_rope(ctypes.byref(a), None) == _lib.SG_OK
+
+
 def test_product_package_never_imports_the_oracle():
     for path in (ROOT / "specgrove_amd").rglob("*.py"):
         text = path.read_text()
