@@ -975,13 +975,16 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
     return nq <= 2 ? 550 + 57 * tiles : 840 + 88 * tiles;
   };
 
-  // Small waves (fewer (request, kv head, row tile) units than the launch has
-  // slots) are latency-bound: every unit of request i is cut into
+  // Small waves (fewer (request, kv head, row tile) units than the GPU has
+  // CUs) are latency-bound: every unit of request i is cut into
   // small_splits[i] key ranges, chosen greedily -- the request whose pieces
-  // cost most gets one more piece -- while the wave stays within `target`
-  // units (one dispatch round, no unit waits for a slot) and pieces keep at
-  // least four tiles of prefix.  No row splits: they would add units.
-  const bool small_wave = base_units > 0 && base_units < target;
+  // cost most gets one more piece -- while the wave stays within one unit
+  // per CU (a lone workgroup streams at its CU's whole bandwidth, and fewer
+  // pieces write fewer partials: 39 us against 44 us at two per CU on a
+  // 16-request, 496-row Qwen3-4B wave) and pieces keep at least four tiles of
+  // prefix.  No row splits: they would add units.
+  const int64_t small_target = target_units_hint > 0 ? target_units_hint : kDefaultCUs;
+  const bool small_wave = base_units > 0 && base_units < small_target;
   std::vector<int> small_splits(num_requests, 1);
   if (small_wave) {
     auto piece_cost = [&](int i, int pieces) -> int64_t {
@@ -1002,7 +1005,7 @@ extern "C" int sg_tree_attn_plan(int32_t num_requests, const int32_t* row_offset
       const int next = small_splits[i] + 1;
       const int64_t add =
           static_cast<int64_t>(num_kv_heads) * ((rows + rows_per_tile - 1) / rows_per_tile);
-      if (total + add > target || prefix_len_host[i] / next < 4 * kTileKeys) continue;
+      if (total + add > small_target || prefix_len_host[i] / next < 4 * kTileKeys) continue;
       small_splits[i] = next;
       total += add;
       heap.push({piece_cost(i, next), i});
