@@ -391,7 +391,10 @@ typedef struct SgQkNormRopeArgs {
 } SgQkNormRopeArgs;
 
 /* Per-head RMSNorm of q and k, rotary embedding of both (rotate-half form,
- * bf16 cos/sin of fp32 angles position * inv_freq), v copied. */
+ * bf16 cos/sin of fp32 angles position * inv_freq), v copied.  The q/k/v rows,
+ * norm weights and outputs are read and written 16 bytes at a time: their
+ * pointers must be 16-byte aligned and qkv_row_stride, q_row_stride and
+ * kv_head_stride multiples of 8 elements (else SG_EINVAL). */
 int sg_qk_norm_rope(const SgQkNormRopeArgs* args, sg_stream_t stream);
 
 /* out[r, :I] = bf16(bf16(silu(gate)) * up) with gate = gate_up[r, :I] and
