@@ -574,10 +574,17 @@ __global__ __launch_bounds__(kWave) void exit_find_kernel(SgTreeSampleArgs a) {
   int j = 0;
   float lp = 0.0f;
   if (s < slabs) {
+    // The slab's line totals in one round trip, then the same sequential scan.
     const float* lt = line_totals + static_cast<int64_t>(s) * kLinesPerSlab;
-    while (j < kLinesPerSlab - 1 && !((slab_prefix + lp) + lt[j] > bound)) {
-      lp = lp + lt[j];
-      ++j;
+    float ltv[kLinesPerSlab];
+#pragma unroll
+    for (int e = 0; e < kLinesPerSlab; ++e) ltv[e] = lt[e];
+#pragma unroll
+    for (int e = 0; e < kLinesPerSlab - 1; ++e) {
+      if (j == e && !((slab_prefix + lp) + ltv[e] > bound)) {
+        lp = lp + ltv[e];
+        j = e + 1;
+      }
     }
   }
   const S* __restrict__ x = static_cast<const S*>(a.logits_dev) + a.logits_row_stride * row;
