@@ -66,6 +66,17 @@ def _check_device_tensor(t: torch.Tensor, name: str, dtype: torch.dtype) -> None
     _require(t.dtype == dtype, f"{name} must be {dtype}, got {t.dtype}")
 
 
+def _check_device_tensors(tensors: tuple, names: tuple, dtype: torch.dtype) -> None:
+    """_check_device_tensor over several tensors of one dtype."""
+    for t in tensors:
+        if not (isinstance(t, torch.Tensor) and t.is_cuda and t.dtype == dtype):
+            break
+    else:
+        return
+    for t, name in zip(tensors, names):
+        _check_device_tensor(t, name, dtype)
+
+
 def _check_rows(t: torch.Tensor, name: str) -> None:
     """bf16 tensors whose last (head) dim is contiguous and 16-byte aligned."""
     _check_device_tensor(t, name, torch.bfloat16)
@@ -311,43 +322,28 @@ def prepare_kv_commit(k_cache_ptrs: torch.Tensor, v_cache_ptrs: torch.Tensor,
     pointer_array); keep_rows [n, keep_stride] i32, keep_len [n] i32,
     prefix_start [n] i64, lengths [n] i32 (advanced in place).
     """
-    for t, name in ((k_cache_ptrs, "k_cache_ptrs"), (v_cache_ptrs, "v_cache_ptrs"),
-                    (k_tree_ptrs, "k_tree_ptrs"), (v_tree_ptrs, "v_tree_ptrs"),
-                    (prefix_start, "prefix_start")):
-        _check_device_tensor(t, name, torch.int64)
-    for t, name in ((row_offset, "row_offset"), (keep_rows, "keep_rows"),
-                    (keep_len, "keep_len"), (lengths, "lengths")):
-        _check_device_tensor(t, name, torch.int32)
+    _check_device_tensors((k_cache_ptrs, v_cache_ptrs, k_tree_ptrs, v_tree_ptrs, prefix_start),
+                          ("k_cache_ptrs", "v_cache_ptrs", "k_tree_ptrs", "v_tree_ptrs",
+                           "prefix_start"), torch.int64)
+    _check_device_tensors((row_offset, keep_rows, keep_len, lengths),
+                          ("row_offset", "keep_rows", "keep_len", "lengths"), torch.int32)
     layers = k_cache_ptrs.numel()
     _require(v_cache_ptrs.numel() == layers and k_tree_ptrs.numel() == layers
              and v_tree_ptrs.numel() == layers, "per-layer pointer arrays disagree")
     _require(keep_rows.dim() == 2 and keep_rows.is_contiguous(), "keep_rows must be [n, stride]")
-    n = keep_rows.shape[0]
+    n, keep_stride = keep_rows.shape
     _require(keep_len.numel() == n and lengths.numel() == n and prefix_start.numel() == n
              and row_offset.numel() == n + 1, "request metadata sizes disagree")
     if status is not None:
         _check_device_tensor(status, "status", torch.int32)
-    a = _lib.SgKvCommitArgs()
-    a.num_layers = layers
-    a.num_requests = n
-    a.num_kv_heads = num_kv_heads
-    a.head_dim = head_dim
-    a.k_cache_layers_dev = k_cache_ptrs.data_ptr()
-    a.v_cache_layers_dev = v_cache_ptrs.data_ptr()
-    a.cache_head_stride = cache_head_stride
-    a.cache_token_stride = cache_token_stride
-    a.k_tree_layers_dev = k_tree_ptrs.data_ptr()
-    a.v_tree_layers_dev = v_tree_ptrs.data_ptr()
-    a.tree_row_stride = tree_row_stride
-    a.tree_head_stride = tree_head_stride
-    a.row_offset_dev = row_offset.data_ptr()
-    a.keep_rows_dev = keep_rows.data_ptr()
-    a.keep_stride = keep_rows.shape[1]
-    a.keep_len_dev = keep_len.data_ptr()
-    a.prefix_start_dev = prefix_start.data_ptr()
-    a.lengths_dev = lengths.data_ptr()
-    a.capacity = capacity
-    a.status_dev = status.data_ptr() if status is not None else 0
+    # Positional, in the order of SgKvCommitArgs' fields.
+    a = _lib.SgKvCommitArgs(
+        layers, n, num_kv_heads, head_dim,
+        k_cache_ptrs.data_ptr(), v_cache_ptrs.data_ptr(), cache_head_stride, cache_token_stride,
+        k_tree_ptrs.data_ptr(), v_tree_ptrs.data_ptr(), tree_row_stride, tree_head_stride,
+        row_offset.data_ptr(), keep_rows.data_ptr(), keep_stride, keep_len.data_ptr(),
+        prefix_start.data_ptr(), lengths.data_ptr(), capacity,
+        status.data_ptr() if status is not None else 0)
     keep = (k_cache_ptrs, v_cache_ptrs, k_tree_ptrs, v_tree_ptrs, row_offset, keep_rows,
             keep_len, prefix_start, lengths, status)
     return PreparedCall("sg_kv_commit", a, keep)
