@@ -41,6 +41,8 @@ Also reported in the same JSON line:
 from __future__ import annotations
 
 import argparse
+import contextlib
+import gc
 import json
 import os
 import statistics
@@ -80,6 +82,23 @@ def parse_args():
     return p.parse_args()
 
 
+@contextlib.contextmanager
+def gc_paused():
+    """Python's cyclic garbage collector held off for a timed region (after
+    one full collection), as timeit does.  With this process's ~170k tracked
+    objects a generation-2 pass takes 15-40 ms on the host; landing inside a
+    back-to-back window it lets the GPU queue run dry and inflates the window
+    (measured: 120 us per attention call read as 350-430 us)."""
+    gc.collect()
+    enabled = gc.isenabled()
+    gc.disable()
+    try:
+        yield
+    finally:
+        if enabled:
+            gc.enable()
+
+
 def _events(torch, n):
     return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
 
@@ -87,11 +106,12 @@ def _events(torch, n):
 def time_calls(torch, fn, iters):
     """Per-call milliseconds from HIP events recorded on the current stream."""
     starts, ends = _events(torch, iters), _events(torch, iters)
-    for k in range(iters):
-        starts[k].record()
-        fn(k)
-        ends[k].record()
-    torch.cuda.synchronize()
+    with gc_paused():
+        for k in range(iters):
+            starts[k].record()
+            fn(k)
+            ends[k].record()
+        torch.cuda.synchronize()
     return [s.elapsed_time(e) for s, e in zip(starts, ends)]
 
 
@@ -99,11 +119,12 @@ def back_to_back(torch, fn, iters):
     """Average milliseconds per call of ``iters`` calls enqueued back to back
     between one pair of HIP events on the current (launch) stream."""
     start, end = _events(torch, 2)
-    start.record()
-    for k in range(iters):
-        fn(k)
-    end.record()
-    torch.cuda.synchronize()
+    with gc_paused():
+        start.record()
+        for k in range(iters):
+            fn(k)
+        end.record()
+        torch.cuda.synchronize()
     return start.elapsed_time(end) / iters
 
 
@@ -196,11 +217,12 @@ def host_costs(torch, ops, wl, plan, meta, sets, iters):
     timed back to back on the GPU."""
     def host_us(fn):
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for k in range(iters):
-            fn(k)
-        us = (time.perf_counter() - t0) / iters * 1e6
-        torch.cuda.synchronize()
+        with gc_paused():
+            t0 = time.perf_counter()
+            for k in range(iters):
+                fn(k)
+            us = (time.perf_counter() - t0) / iters * 1e6
+            torch.cuda.synchronize()
         return us
     attn = [ops.prepare_tree_attention(st["q"], st["kc"], st["vc"], st["kt"], st["vt"],
                                        meta["row_offset"], meta["prefix_start"],
@@ -246,11 +268,12 @@ def commit_all_layers(torch, np, ops, wl, meta, device, layers=36, iters=50, war
         call(k)
     torch.cuda.synchronize()
     st, en = _events(torch, 2)
-    st.record()
-    for k in range(iters):
-        call(k)
-    en.record()
-    torch.cuda.synchronize()
+    with gc_paused():
+        st.record()
+        for k in range(iters):
+            call(k)
+        en.record()
+        torch.cuda.synchronize()
     us = st.elapsed_time(en) / iters * 1e3
     rows = int(sum(len(k) for k in wl.keep))
     del arena_k, arena_v, tree_k, tree_v
@@ -444,11 +467,12 @@ def verify_wave_bench(torch, np, W, ops, wl, hidden, weight, device, iters=5):
                      ("every_row_library_gemm_us", library_full)):
         fn()
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(iters):
-            fn()
-        torch.cuda.synchronize()
-        out[name] = (time.perf_counter() - t0) / iters * 1e6
+        with gc_paused():
+            t0 = time.perf_counter()
+            for _ in range(iters):
+                fn()
+            torch.cuda.synchronize()
+            out[name] = (time.perf_counter() - t0) / iters * 1e6
     return out
 
 
@@ -678,20 +702,22 @@ def main():
         step(k)
     torch.cuda.synchronize()
     start, end = _events(torch, 2)
-    start.record()
-    for k in range(steps):
-        step(k)
-    end.record()
-    torch.cuda.synchronize()
+    with gc_paused():
+        start.record()
+        for k in range(steps):
+            step(k)
+        end.record()
+        torch.cuda.synchronize()
     ms_per_step = start.elapsed_time(end) / steps
 
     # Host time to enqueue one step (argument checks, ctypes, launches); the
     # GPU runs behind, so this is the host's share, not the step's duration.
-    t0 = time.perf_counter()
-    for k in range(steps):
-        step(k)
-    host_us = (time.perf_counter() - t0) / steps * 1e6
-    torch.cuda.synchronize()
+    with gc_paused():
+        t0 = time.perf_counter()
+        for k in range(steps):
+            step(k)
+        host_us = (time.perf_counter() - t0) / steps * 1e6
+        torch.cuda.synchronize()
 
     attn_call = lambda k: attention_call(ops, wl, plan, meta, sets[k % N_SETS])  # noqa: E731
     attn_b2b = back_to_back(torch, attn_call, steps)
