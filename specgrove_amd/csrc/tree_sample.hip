@@ -103,6 +103,60 @@ __device__ __forceinline__ void load4(const S* __restrict__ p, float out[4]) {
   }
 }
 
+// Buffer resource over one logits row (vocab elements from x).  Third word:
+// the gfx9 raw-buffer format (32-bit data, no swizzle, offset addressing).
+template <typename S>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const S* x, int vocab) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<S*>(x), static_cast<short>(0),
+                                           vocab * static_cast<int>(sizeof(S)), 0x00020000);
+}
+
+// load_slab<S, true, true> through a row's buffer resource, for slabs that
+// may lie partly or wholly past the row: a load past the row's end returns
+// zeros without a memory access, and the masking of tokens >= vocab is plain
+// arithmetic.  With no branch around the loads a wave can prefetch its next
+// slab unconditionally; a branch there makes the compiler wait for every
+// outstanding load (the prefetch included) before the current slab's
+// arithmetic.
+constexpr int kBufNonTemporal = 2;  // the slc bit: `nt` on gfx950
+template <typename S>
+__device__ __forceinline__ void load_slab_rsrc(__amdgpu_buffer_rsrc_t rs, int vocab, int slab,
+                                               int lane, float v[32]) {
+  const int base = slab * kSlab + 4 * lane;
+#pragma unroll
+  for (int j = 0; j < kLinesPerSlab; ++j) {
+    const int off = (base + kLine * j) * static_cast<int>(sizeof(S));
+    if constexpr (sizeof(S) == 4) {
+      const floatx4 q = __builtin_bit_cast(
+          floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kBufNonTemporal));
+      v[4 * j + 0] = q[0];
+      v[4 * j + 1] = q[1];
+      v[4 * j + 2] = q[2];
+      v[4 * j + 3] = q[3];
+    } else {
+      const uintx2 q = __builtin_bit_cast(
+          uintx2, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, kBufNonTemporal));
+      v[4 * j + 0] = to_f32(half_at<S>(q[0], 0));
+      v[4 * j + 1] = to_f32(half_at<S>(q[0], 1));
+      v[4 * j + 2] = to_f32(half_at<S>(q[1], 0));
+      v[4 * j + 3] = to_f32(half_at<S>(q[1], 1));
+    }
+  }
+}
+
+// Tokens >= vocab of slab s read as -inf (vocab is a multiple of 4 on the
+// vector path, so each lane's 4-token chunk is wholly in or out).
+__device__ __forceinline__ void mask_slab_tail(int vocab, int slab, int lane, float v[32]) {
+  if ((slab + 1) * kSlab <= vocab) return;
+  const int base = slab * kSlab + 4 * lane;
+#pragma unroll
+  for (int j = 0; j < kLinesPerSlab; ++j) {
+    const bool out = base + kLine * j >= vocab;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) v[4 * j + c] = out ? -__builtin_inff() : v[4 * j + c];
+  }
+}
+
 // Lane l of the wave loads tokens 2048*s + 256*j + 4*l + c into v[4*j + c];
 // tokens at or beyond vocab read as -inf (they contribute E = 0).
 template <typename S, bool kVec, bool kStream = false>
@@ -184,8 +238,36 @@ __global__ __launch_bounds__(kStatsThreads, 2) void row_stats_kernel(
   constexpr int kWavesPerRow = kStatsThreads / kWave;
   float v[32], w[32];
   int s = wave;
-  if (s < slabs) load_slab<S, kVec, true>(x, vocab, s, lane, v);
-  while (s < slabs) {
+  if constexpr (kVec) {
+    // Steady loop with an unconditional prefetch of the wave's next slab.
+    const __amdgpu_buffer_rsrc_t rs = row_rsrc(x, vocab);
+    if (s < slabs) {
+      load_slab_rsrc<S>(rs, vocab, s, lane, v);
+      while (true) {
+        load_slab_rsrc<S>(rs, vocab, s + kWavesPerRow, lane, w);
+        mask_slab_tail(vocab, s, lane, v);
+        const MZ a = slab_stats(v);
+        if (lane == 0) {
+          s_m[s] = a.m;
+          s_z[s] = a.z;
+        }
+        s += kWavesPerRow;
+        if (s >= slabs) break;
+        load_slab_rsrc<S>(rs, vocab, s + kWavesPerRow, lane, v);
+        mask_slab_tail(vocab, s, lane, w);
+        const MZ b = slab_stats(w);
+        if (lane == 0) {
+          s_m[s] = b.m;
+          s_z[s] = b.z;
+        }
+        s += kWavesPerRow;
+        if (s >= slabs) break;
+      }
+    }
+    s = slabs;  // the loop below is the unaligned path's
+  }
+  if (!kVec && s < slabs) load_slab<S, kVec, true>(x, vocab, s, lane, v);
+  while (!kVec && s < slabs) {
     const int next = s + kWavesPerRow;
     if (next < slabs) load_slab<S, kVec, true>(x, vocab, next, lane, w);
     const MZ a = slab_stats(v);
