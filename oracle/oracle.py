@@ -514,16 +514,25 @@ def kv_split(prefix_k: np.ndarray, prefix_v: np.ndarray, tree_k: np.ndarray,
 
 
 def cpu_model() -> str:
-    """The host CPU's model name (from /proc/cpuinfo when available)."""
+    """The host CPU's model name from /proc/cpuinfo, with its family, model
+    and stepping numbers (a virtual machine may report only a generic name
+    such as "AMD EPYC")."""
+    fields = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if not line.strip():
+                    break  # the first processor's block is enough
+                key, _, value = line.partition(":")
+                fields[key.strip()] = value.strip()
     except OSError:
         pass
-    import platform
-    return platform.processor() or platform.machine()
+    name = fields.get("model name")
+    if not name:
+        import platform
+        return platform.processor() or platform.machine()
+    ids = [f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields]
+    return f"{name} ({', '.join(ids)})" if ids else name
 
 
 def cpu_threads() -> int:
