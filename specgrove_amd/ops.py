@@ -233,18 +233,19 @@ def prepare_tree_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     for t, name in ((q, "q"), (k_cache, "k_cache"), (v_cache, "v_cache"),
                     (k_tree, "k_tree"), (v_tree, "v_tree")):
         _check_rows(t, name)
-    _check_device_tensor(row_offset, "row_offset", torch.int32)
+    _check_device_tensors((row_offset, prefix_len, parent),
+                          ("row_offset", "prefix_len", "parent"), torch.int32)
     _check_device_tensor(prefix_start, "prefix_start", torch.int64)
-    _check_device_tensor(prefix_len, "prefix_len", torch.int32)
-    _check_device_tensor(parent, "parent", torch.int32)
     _require(q.dim() == 3 and k_tree.dim() == 3 and k_cache.dim() == 3,
              "q/k_tree must be [R, H, D] and k_cache [Hkv, tokens, D]")
     rows, hq, dim = q.shape
     hkv = k_cache.shape[0]
-    _require(k_cache.shape == v_cache.shape and k_cache.stride() == v_cache.stride(),
+    cache_strides = k_cache.stride()
+    tree_strides = k_tree.stride()
+    _require(k_cache.shape == v_cache.shape and cache_strides == v_cache.stride(),
              "k_cache and v_cache must share shape and strides")
     _require(k_tree.shape == (rows, hkv, dim) and v_tree.shape == k_tree.shape
-             and k_tree.stride() == v_tree.stride(),
+             and tree_strides == v_tree.stride(),
              "k_tree/v_tree must be [R, Hkv, D] with equal strides")
     _require(k_cache.shape[2] == dim, "head dims disagree")
     n = prefix_len.numel()
@@ -259,34 +260,21 @@ def prepare_tree_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
         out = torch.empty((rows, hq, dim), dtype=torch.bfloat16, device=q.device)
     _check_rows(out, "out")
     _require(out.shape == (rows, hq, dim), "out must be [R, Hq, D]")
-    a = _lib.SgTreeAttnArgs()
-    a.num_requests = n
-    a.num_rows = rows
-    a.num_q_heads = hq
-    a.num_kv_heads = hkv
-    a.head_dim = dim
-    a.scale = float(dim ** -0.5 if scale is None else scale)
-    a.q_dev = q.data_ptr()
-    a.q_row_stride, a.q_head_stride = q.stride(0), q.stride(1)
-    a.k_cache_dev = k_cache.data_ptr()
-    a.v_cache_dev = v_cache.data_ptr()
-    a.cache_head_stride, a.cache_token_stride = k_cache.stride(0), k_cache.stride(1)
-    a.k_tree_dev = k_tree.data_ptr()
-    a.v_tree_dev = v_tree.data_ptr()
-    a.tree_row_stride, a.tree_head_stride = k_tree.stride(0), k_tree.stride(1)
-    a.row_offset_dev = row_offset.data_ptr()
-    a.prefix_start_dev = prefix_start.data_ptr()
-    a.prefix_len_dev = prefix_len.data_ptr()
-    a.parent_dev = parent.data_ptr()
-    a.out_dev = out.data_ptr()
-    a.out_row_stride, a.out_head_stride = out.stride(0), out.stride(1)
-    a.plan_dev = plan.device.data_ptr()
-    a.plan_host = plan.host.ctypes.data
-    a.status_dev = status.data_ptr() if status is not None else 0
-    a.plan_units = plan.units
-    a.plan_merges = plan.merges
-    a.workspace_dev = plan.workspace.data_ptr() if plan.workspace is not None else 0
-    a.workspace_bytes = plan.workspace.numel() if plan.workspace is not None else 0
+    q_strides = q.stride()
+    out_strides = out.stride()
+    workspace = plan.workspace
+    # Positional, in the order of SgTreeAttnArgs' fields.
+    a = _lib.SgTreeAttnArgs(
+        n, rows, hq, hkv, dim, float(dim ** -0.5 if scale is None else scale),
+        q.data_ptr(), q_strides[0], q_strides[1],
+        k_cache.data_ptr(), v_cache.data_ptr(), cache_strides[0], cache_strides[1],
+        k_tree.data_ptr(), v_tree.data_ptr(), tree_strides[0], tree_strides[1],
+        row_offset.data_ptr(), prefix_start.data_ptr(), prefix_len.data_ptr(),
+        parent.data_ptr(), out.data_ptr(), out_strides[0], out_strides[1],
+        plan.device.data_ptr(), plan.host.ctypes.data, plan.units, plan.merges,
+        workspace.data_ptr() if workspace is not None else 0,
+        workspace.numel() if workspace is not None else 0,
+        status.data_ptr() if status is not None else 0)
     keep = (q, k_cache, v_cache, k_tree, v_tree, row_offset, prefix_start, prefix_len, parent,
             plan, out, status)
     return PreparedCall("sg_tree_attn_fwd", a, keep, result=out)
