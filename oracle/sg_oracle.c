@@ -23,10 +23,12 @@
  * computes in fp32 with its own exp and a fixed reduction order so that the
  * CPU and the GPU produce the same bits.  The order is:
  *
- *   exp:   E(x) = 0 for x < -87 (or NaN); otherwise Cody-Waite reduction
- *          x = n*ln2 + r (n = rint(x*log2e), ln2 split hi/lo, both by fma),
- *          degree-6 Taylor polynomial for e^r in Horner form with fma, and an
- *          exact scale by 2^n built from the exponent bits.
+ *   exp:   x clamped to [-120, 88] (NaN and -inf to -120; above 88: +inf);
+ *          Cody-Waite reduction x = n*ln2 + r (n = rint(x*log2e), ln2 split
+ *          hi/lo, both by fma); a degree-5 polynomial for e^r (coefficients
+ *          fitted for relative error) in Horner form with fma; p * 2^n with
+ *          one rounding (exactly 0 below about -103.3, subnormal down from
+ *          -87.3).
  *   token t of a row is addressed as t = 2048*s + 256*j + 4*l + c
  *          (slab s, line j in [0,8), lane l in [0,64), component c in [0,4)).
  *   row stats (m, Z):
@@ -61,34 +63,43 @@
 #define SGO_LOG2E 0x1.715476p+0f
 #define SGO_LN2_HI 0x1.62e4p-1f
 #define SGO_LN2_LO 0x1.7f7d1cp-20f
-#define SGO_C6 0x1.6c16c2p-10f
-#define SGO_C5 0x1.111112p-7f
-#define SGO_C4 0x1.555556p-5f
-#define SGO_C3 0x1.555556p-3f
-#define SGO_EXP_LO (-87.0f)
+#define SGO_C5 0x1.10625ap-7f
+#define SGO_C4 0x1.5729eep-5f
+#define SGO_C3 0x1.5557aep-3f
+#define SGO_C2 0x1.fffdfcp-2f
+#define SGO_EXP_LO (-120.0f)
 #define SGO_EXP_HI 88.0f
 
 /* Error codes shared with the product ABI. */
 #define SGO_OK 0
 #define SGO_EINVAL (-1)
 
+/* 2^e for e in [-126, 127], from the exponent bits. */
+static float sgo_pow2(int e) {
+  int32_t bits = (e + 127) << 23;
+  float v;
+  memcpy(&v, &bits, sizeof(v));
+  return v;
+}
+
 float sgo_exp(float x) {
-  if (!(x >= SGO_EXP_LO)) return 0.0f;
   if (x > SGO_EXP_HI) return INFINITY;
-  float n = rintf(x * SGO_LOG2E);
-  float r = fmaf(-n, SGO_LN2_HI, x);
+  /* fmaxf returns the other operand for a NaN: NaN and -inf clamp to -120. */
+  float xc = fmaxf(x, SGO_EXP_LO);
+  float n = rintf(xc * SGO_LOG2E);
+  float r = fmaf(-n, SGO_LN2_HI, xc);
   r = fmaf(-n, SGO_LN2_LO, r);
-  float p = SGO_C6;
-  p = fmaf(p, r, SGO_C5);
+  float p = SGO_C5;
   p = fmaf(p, r, SGO_C4);
   p = fmaf(p, r, SGO_C3);
-  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, SGO_C2);
   p = fmaf(p, r, 1.0f);
   p = fmaf(p, r, 1.0f);
-  int32_t bits = ((int32_t)n + 127) << 23;
-  float scale;
-  memcpy(&scale, &bits, sizeof(scale));
-  return p * scale;
+  int e = (int)n;
+  /* p * 2^n with one rounding: an exact scale into the normal range, then
+     (below 2^-126) a second exact-operand product that rounds once. */
+  if (e >= -126) return p * sgo_pow2(e);
+  return (p * sgo_pow2(e + 64)) * sgo_pow2(-64);
 }
 
 typedef struct {

@@ -44,10 +44,11 @@ def _check_case(case, device, oracle):
 
 def test_exp_bit_exact(device, oracle):
     xs = np.concatenate([
-        np.linspace(-90, 1, 200001, dtype=np.float32),
+        np.linspace(-130, 1, 400001, dtype=np.float32),
         np.array([0.0, -0.0, -87.0, np.nextafter(np.float32(-87.0), np.float32(0)),
                   np.nextafter(np.float32(-87.0), np.float32(-100)), -1e-30, 1e-30,
-                  -np.inf, np.nan, 88.0, 89.0], np.float32),
+                  -103.0, -103.3, -104.0, -120.0, -121.0, -1e30,
+                  -np.inf, np.nan, 88.0, 89.0, np.inf], np.float32),
         -np.abs(np.random.default_rng(0).standard_normal(100000).astype(np.float32) * 30),
     ])
     got = ops.exp_probe(torch.from_numpy(xs).to(device)).cpu().numpy()

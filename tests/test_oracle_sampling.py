@@ -23,9 +23,21 @@ def test_exp_matches_float64_exp(oracle):
     ref = np.exp(x.astype(np.float64))
     assert np.max(np.abs(e - ref) / ref) < 4e-7
     assert np.all(np.diff(e) >= 0), "exp must be monotone"
-    assert oracle.exp_f32(np.array([0.0], np.float32))[0] == 1.0
-    low = oracle.exp_f32(np.array([-87.01, -100.0, -np.inf, np.nan], np.float32))
+    assert oracle.exp_f32(np.array([0.0, -0.0], np.float32)).tolist() == [1.0, 1.0]
+    # Into the subnormal range: monotone, within 4e-7 relative or one
+    # subnormal step (2^-149) of exp, below 2^-126 from -87.5 down, and
+    # exactly 0 below about -103.3 (NaN and -inf included).
+    deep = np.linspace(-110.0, -87.0, 200_001, dtype=np.float32)
+    ed = oracle.exp_f32(deep)
+    ref = np.exp(deep.astype(np.float64))
+    assert np.all(np.diff(ed) >= 0)
+    assert np.all(np.abs(ed - ref) <= np.maximum(4e-7 * ref, 2.0 ** -149))
+    assert np.all(ed[deep <= -87.5] < np.float32(2.0 ** -126))
+    low = oracle.exp_f32(np.array([-104.5, -120.0, -1000.0, -np.inf, np.nan], np.float32))
     assert np.all(low == 0.0)
+    assert oracle.exp_f32(np.array([-100.0], np.float32))[0] > 0.0
+    high = oracle.exp_f32(np.array([88.0, 88.5, np.inf], np.float32))
+    assert np.isfinite(high[0]) and np.all(np.isinf(high[1:]))
 
 
 @pytest.mark.parametrize("vocab", [1, 7, 2048, 2049, 4096, 151936])
