@@ -179,3 +179,18 @@ def test_oracle_rejects_short_uniforms(oracle):
     with pytest.raises(ValueError):
         oracle.tree_sample(case["logits"], case["row_offset"], case["parent"], case["token"],
                            case["uniforms"][:, :1], case["max_depth"])
+
+
+def test_exp_coefficients_are_the_fitted_ones():
+    """The polynomial constants of the GPU header and of the C restatement are
+    the binary32 rounding of oracle/fit_exp_poly.py's relative-error fit."""
+    import re
+    from oracle.fit_exp_poly import fit
+    root = Path(__file__).resolve().parents[1]
+    fitted = [float(v) for v in fit().astype(np.float32)]
+    for path, prefix in ((root / "specgrove_amd/csrc/sg_math.h", "SG_C"),
+                         (root / "oracle/sg_oracle.c", "SGO_C")):
+        text = path.read_text()
+        got = [float.fromhex(re.search(rf"#define {prefix}{j} (\S+)f", text).group(1))
+               for j in range(2, 6)]
+        assert got == fitted, path
