@@ -228,3 +228,33 @@ def test_reused_outputs_must_fit_the_call(device, oracle):
         case["uniforms"], case["max_depth"])
     np.testing.assert_array_equal(res.accept_len.cpu().numpy(), length)
     np.testing.assert_array_equal(res.bonus.cpu().numpy(), bonus)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("vocab,pad", [(6144, 64), (4100, 4), (4099, 1), (3000, 17)])
+def test_padded_logits_rows(device, oracle, dtype, vocab, pad):
+    """Logits rows inside a wider buffer (row stride above the vocabulary):
+    the statistics and the draw read only the first `vocab` tokens of each
+    row, on the 4-token vector path (stride and vocab multiples of 4) and on
+    the element path, bit-exact against the oracle on the same tokens."""
+    case = tree_problem(600 + vocab + pad, num_requests=5, nodes=[7, 1, 12, 4, 9], vocab=vocab)
+    rows = case["logits"].shape[0]
+    wide = torch.full((rows, vocab + pad), float("nan"), dtype=torch.float32)
+    wide[:, :vocab] = torch.from_numpy(case["logits"])
+    logits = wide.to(dtype).to(device)[:, :vocab]
+    assert logits.stride(0) == vocab + pad
+    res = ops.tree_sample(logits, torch.from_numpy(case["row_offset"]).to(device),
+                          torch.from_numpy(case["parent"]).to(device),
+                          torch.from_numpy(case["token"]).to(device),
+                          torch.from_numpy(case["uniforms"]).to(device), case["max_depth"])
+    torch.cuda.synchronize()
+    widened = logits.float().cpu().numpy()
+    nodes, length, bonus, m, z = oracle.tree_sample(
+        widened, case["row_offset"], case["parent"], case["token"], case["uniforms"],
+        case["max_depth"])
+    assert int(res.status.item()) == 0
+    np.testing.assert_array_equal(res.row_max.cpu().numpy(), m)
+    assert np.array_equal(res.row_sum.cpu().numpy().view(np.uint32), z.view(np.uint32))
+    np.testing.assert_array_equal(res.accept_len.cpu().numpy(), length)
+    np.testing.assert_array_equal(res.accept_nodes.cpu().numpy()[:, :case["max_depth"]], nodes)
+    np.testing.assert_array_equal(res.bonus.cpu().numpy(), bonus)
