@@ -221,17 +221,17 @@ def tree_verify_hip_lazy_projection_batched(parents_batch: Sequence[Sequence[int
     device = hidden.device
     row_offset = np.zeros(count + 1, np.int32)
     np.cumsum(rows, out=row_offset[1:])
-    # Internal nodes (those with children) in ascending packed order.
-    row_map = np.full(total, -1, np.int32)
-    internal_counts = []
-    for i, (parents, _, _) in enumerate(topologies):
-        internal = sorted(set(parents[1:]))
-        internal_counts.append(len(internal))
-        for node in internal:
-            row_map[row_offset[i] + node] = 0
-    internal_rows = np.flatnonzero(row_map >= 0).astype(np.int32)
-    row_map[internal_rows] = np.arange(internal_rows.size, dtype=np.int32)
     parent = np.concatenate([np.asarray(p, np.int32) for p, _, _ in topologies])
+    # Internal nodes (those with children) in ascending packed order: every
+    # node that is some node's parent, in packed numbering.
+    owner = np.repeat(np.arange(count, dtype=np.int32), rows)
+    has_parent = parent >= 0
+    internal = np.zeros(total, bool)
+    internal[parent[has_parent] + row_offset[owner[has_parent]]] = True
+    internal_rows = np.flatnonzero(internal).astype(np.int32)
+    internal_counts = np.bincount(owner[internal_rows], minlength=count).tolist()
+    row_map = np.full(total, -1, np.int32)
+    row_map[internal_rows] = np.arange(internal_rows.size, dtype=np.int32)
     token = np.concatenate([np.asarray([-1] + list(t), np.int32) for _, t, _ in topologies])
     meta = torch.from_numpy(np.concatenate([row_offset, parent, token, row_map,
                                             internal_rows])).to(device)
@@ -242,8 +242,6 @@ def tree_verify_hip_lazy_projection_batched(parents_batch: Sequence[Sequence[int
     meta_row_map = meta[n1 + 2 * total:n1 + 3 * total]
     meta_internal = meta[n1 + 3 * total:]
 
-    uniforms, max_depth = _draw_uniforms(topologies, generators, device)
-
     def projection_valid(head: "ops.LmHeadResult") -> torch.Tensor:
         ok = (torch.isfinite(head.row_max).all() & torch.isfinite(head.row_sum).all()
               & (head.row_sum > 0).all() & (head.status == 0).all())
@@ -251,6 +249,10 @@ def tree_verify_hip_lazy_projection_batched(parents_batch: Sequence[Sequence[int
 
     if internal_rows.size:
         head = ops.lm_head(hidden, weight, meta_internal)
+    # Drawn after the projection is enqueued: the per-request draws queue
+    # behind it on the stream, and their host work overlaps its run.
+    uniforms, max_depth = _draw_uniforms(topologies, generators, device)
+    if internal_rows.size:
         logits, row_max, row_sum = head.logits, head.row_max, head.row_sum
         valid = projection_valid(head)
     else:  # no tree has an edge: every walk ends at its (unprojected) root
