@@ -64,6 +64,28 @@ def _draw_uniforms(topologies, generators, device):
     return uniforms, max_depth
 
 
+_SIDE_STREAMS: dict = {}
+
+
+def _draw_uniforms_beside(topologies, generators, device):
+    """_draw_uniforms on a side stream (default priority, one per device), so
+    that the per-request draws -- many tiny launches -- run beside the work
+    already queued on the current stream instead of after it.  They read
+    nothing the current stream writes (a generator's state lives on the host)
+    and write only their own new tensor, so the side stream waits for
+    nothing; the current stream waits for them before anything it enqueues
+    later."""
+    main = torch.cuda.current_stream(device)
+    side = _SIDE_STREAMS.get(main.device_index)
+    if side is None:
+        side = _SIDE_STREAMS[main.device_index] = torch.cuda.Stream(device)
+    with torch.cuda.stream(side):
+        uniforms, max_depth = _draw_uniforms(topologies, generators, device)
+    main.wait_stream(side)
+    uniforms.record_stream(main)
+    return uniforms, max_depth
+
+
 def tree_verify_hip_rejection_batched(parents_batch: Sequence[Sequence[int]],
                                       tokens_batch: Sequence[Sequence[int]],
                                       all_logits: torch.Tensor, temperature: float = 1.0,
@@ -114,7 +136,8 @@ def tree_verify_hip_rejection_batched(parents_batch: Sequence[Sequence[int]],
         raise FloatingPointError("Invalid Target logits for the HIP tree verifier")
 
     device = logits.device
-    uniforms, max_depth = _draw_uniforms(topologies, generators, device)
+    # Beside the work that produces the logits, when that is still running.
+    uniforms, max_depth = _draw_uniforms_beside(topologies, generators, device)
     row_offset = np.zeros(count + 1, np.int32)
     np.cumsum(rows, out=row_offset[1:])
     parent = np.concatenate([np.asarray(p, np.int32) for p, _, _ in topologies])
@@ -249,9 +272,9 @@ def tree_verify_hip_lazy_projection_batched(parents_batch: Sequence[Sequence[int
 
     if internal_rows.size:
         head = ops.lm_head(hidden, weight, meta_internal)
-    # Drawn after the projection is enqueued: the per-request draws queue
-    # behind it on the stream, and their host work overlaps its run.
-    uniforms, max_depth = _draw_uniforms(topologies, generators, device)
+    # Drawn after the projection is enqueued, on a side stream: their host
+    # work and their tiny kernels both overlap the projection.
+    uniforms, max_depth = _draw_uniforms_beside(topologies, generators, device)
     if internal_rows.size:
         logits, row_max, row_sum = head.logits, head.row_max, head.row_sum
         valid = projection_valid(head)
