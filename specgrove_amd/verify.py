@@ -186,6 +186,58 @@ def _head_weight(lm_head) -> torch.Tensor:
     return weight if weight.stride(1) == 1 else weight.contiguous()
 
 
+def _lazy_hidden(final_hidden: torch.Tensor, count: int, rows: Sequence[int], weight):
+    """The packed [R, H] rows of final_hidden when its shape fits the trees'
+    row counts and the head's hidden size, else None (the caller's checks
+    raise)."""
+    total = sum(rows)
+    hidden_size = final_hidden.shape[-1]
+    if final_hidden.dim() == 3 and final_hidden.shape[0] == count and count > 1:
+        if any(r != final_hidden.shape[1] for r in rows):
+            return None
+        hidden = final_hidden.reshape(count * final_hidden.shape[1], hidden_size)
+    elif final_hidden.dim() == 3 and final_hidden.shape[0] == 1:
+        hidden = final_hidden[0]
+    elif final_hidden.dim() == 2:
+        hidden = final_hidden
+    else:
+        return None
+    if hidden.shape[0] != total or hidden_size != weight.shape[1]:
+        return None
+    return hidden if hidden.stride(1) == 1 else hidden.contiguous()
+
+
+def _lazy_meta(parents_batch, tokens_batch):
+    """The lazy walk's packed metadata from the trees' parent and token lists:
+    row_offset [n+1], parent [R], token [R] (-1 at each root), row_map [R]
+    (each node's row among the projected internal rows, else -1), the
+    internal rows' packed indices, and each row's request.  Edges that are not
+    parent < node are skipped, so lists that the topology check would reject
+    still give in-range indices; raises TypeError or ValueError when the lists
+    do not convert to integers."""
+    rows = [len(p) for p in parents_batch]
+    count = len(rows)
+    if count < 1 or min(rows) < 1 or len(tokens_batch) != count:
+        raise ValueError("not a batch of trees")
+    total = sum(rows)
+    row_offset = np.zeros(count + 1, np.int32)
+    np.cumsum(rows, out=row_offset[1:])
+    parent = np.concatenate([np.asarray(p, np.int32).reshape(-1) for p in parents_batch])
+    token = np.concatenate([np.asarray([-1] + list(t), np.int32).reshape(-1)
+                            for t in tokens_batch])
+    if parent.size != total or token.size != total:
+        raise ValueError("not a batch of trees")
+    owner = np.repeat(np.arange(count, dtype=np.int32), rows)
+    local = np.arange(total, dtype=np.int32) - row_offset[owner]
+    edge = (parent >= 0) & (parent < local)
+    internal = np.zeros(total, bool)
+    internal[parent[edge] + row_offset[owner[edge]]] = True
+    internal_rows = np.flatnonzero(internal).astype(np.int32)
+    row_map = np.full(total, -1, np.int32)
+    row_map[internal_rows] = np.arange(internal_rows.size, dtype=np.int32)
+    return row_offset, parent, token, row_map, internal_rows, owner
+
+
 def tree_verify_hip_lazy_projection_batched(parents_batch: Sequence[Sequence[int]],
                                             tokens_batch: Sequence[Sequence[int]],
                                             final_hidden: torch.Tensor, lm_head,
@@ -219,6 +271,24 @@ def tree_verify_hip_lazy_projection_batched(parents_batch: Sequence[Sequence[int
     if probability_dtype != torch.float32:
         raise ValueError("The HIP lazy projection uses fp32 probability arithmetic")
     weight = _head_weight(lm_head)
+    # The internal-row projection is started before the host-side validation
+    # below, so that the two overlap.  Its row indices come from the
+    # unvalidated parents (non-edges skipped, every index in range; the kernel
+    # also bounds-checks each one); an invalid call then raises below, with
+    # the same errors in the same order, before anything is sampled.
+    # The metadata goes to the device first (a synchronous copy, while the GPU
+    # has nothing of this call queued).
+    early, early_meta, early_head = None, None, None
+    try:
+        early_hidden = _lazy_hidden(final_hidden, count, [len(p) for p in parents_batch], weight)
+        if early_hidden is not None:
+            early = _lazy_meta(parents_batch, tokens_batch)
+            early_meta = torch.from_numpy(np.concatenate(early[:5])).to(early_hidden.device)
+            if early[4].size:
+                n1, tot = count + 1, early[1].size
+                early_head = ops.lm_head(early_hidden, weight, early_meta[n1 + 3 * tot:])
+    except (TypeError, ValueError, OverflowError):
+        early, early_meta, early_head = None, None, None  # the checks below raise
     topologies = [_topology(p, t) for p, t in zip(parents_batch, tokens_batch)]
     rows = [len(p) for p, _, _ in topologies]
     total = sum(rows)
@@ -242,22 +312,17 @@ def tree_verify_hip_lazy_projection_batched(parents_batch: Sequence[Sequence[int
         raise ValueError("Tree token is outside the Target vocabulary")
 
     device = hidden.device
-    row_offset = np.zeros(count + 1, np.int32)
-    np.cumsum(rows, out=row_offset[1:])
-    parent = np.concatenate([np.asarray(p, np.int32) for p, _, _ in topologies])
-    # Internal nodes (those with children) in ascending packed order: every
-    # node that is some node's parent, in packed numbering.
-    owner = np.repeat(np.arange(count, dtype=np.int32), rows)
-    has_parent = parent >= 0
-    internal = np.zeros(total, bool)
-    internal[parent[has_parent] + row_offset[owner[has_parent]]] = True
-    internal_rows = np.flatnonzero(internal).astype(np.int32)
+    # Internal nodes (those with children) in ascending packed order.  The
+    # trees are valid now, so the metadata built before the checks is theirs.
+    if early_meta is not None:
+        row_offset, parent, token, row_map, internal_rows, owner = early
+        meta = early_meta
+    else:
+        row_offset, parent, token, row_map, internal_rows, owner = _lazy_meta(
+            [p for p, _, _ in topologies], [t for _, t, _ in topologies])
+        meta = torch.from_numpy(np.concatenate([row_offset, parent, token, row_map,
+                                                internal_rows])).to(device)
     internal_counts = np.bincount(owner[internal_rows], minlength=count).tolist()
-    row_map = np.full(total, -1, np.int32)
-    row_map[internal_rows] = np.arange(internal_rows.size, dtype=np.int32)
-    token = np.concatenate([np.asarray([-1] + list(t), np.int32) for _, t, _ in topologies])
-    meta = torch.from_numpy(np.concatenate([row_offset, parent, token, row_map,
-                                            internal_rows])).to(device)
     n1 = count + 1
     meta_row_offset = meta[:n1]
     meta_parent = meta[n1:n1 + total]
@@ -271,7 +336,8 @@ def tree_verify_hip_lazy_projection_batched(parents_batch: Sequence[Sequence[int
         return ok.to(torch.int32).reshape(1)
 
     if internal_rows.size:
-        head = ops.lm_head(hidden, weight, meta_internal)
+        head = early_head if early_head is not None else ops.lm_head(hidden, weight,
+                                                                     meta_internal)
     # Drawn after the projection is enqueued, on a side stream: their host
     # work and their tiny kernels both overlap the projection.
     uniforms, max_depth = _draw_uniforms_beside(topologies, generators, device)

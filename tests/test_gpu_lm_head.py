@@ -167,3 +167,32 @@ def test_lazy_projection_equals_full_projection_and_oracle(device, oracle, seed)
                                                      .to(device)])
     assert torch.equal(part.row_sum, full_head.row_sum[torch.from_numpy(internal_rows).long()
                                                        .to(device)])
+
+
+def test_lazy_projection_rejects_bad_calls_after_starting_the_projection(device):
+    """The verifier starts the internal-row projection before validating the
+    trees; a bad tree, token or hidden shape still raises the same error,
+    and the generators are left untouched."""
+    sizes = [4, 3, 5]
+    parents, tokens, hidden, weight = _wave(device, 7, sizes)
+    gens = [torch.Generator(device=device).manual_seed(70 + i) for i in range(len(sizes))]
+    states = [g.get_state().clone() for g in gens]
+    bad_parent = [list(p) for p in parents]
+    bad_parent[1][2] = 5                       # a parent after its node
+    with pytest.raises(ValueError, match="Invalid probability-tree topology"):
+        verify.tree_verify_hip_lazy_projection_batched(bad_parent, tokens, hidden, weight,
+                                                       generators=gens)
+    bad_token = [list(t) for t in tokens]
+    bad_token[2][0] = weight.shape[0]
+    with pytest.raises(ValueError, match="outside the Target vocabulary"):
+        verify.tree_verify_hip_lazy_projection_batched(parents, bad_token, hidden, weight,
+                                                       generators=gens)
+    with pytest.raises(ValueError, match="hidden shape mismatch"):
+        verify.tree_verify_hip_lazy_projection_batched(parents, tokens, hidden[:-1], weight,
+                                                       generators=gens)
+    torch.cuda.synchronize()
+    assert all(torch.equal(g.get_state(), s) for g, s in zip(gens, states))
+    # A good call after the bad ones is unaffected.
+    lazy = verify.tree_verify_hip_lazy_projection_batched(parents, tokens, hidden, weight,
+                                                          generators=gens)
+    assert len(lazy) == len(sizes)
