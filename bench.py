@@ -441,7 +441,9 @@ def verify_wave_bench(torch, np, W, ops, wl, hidden, weight, device, iters=5):
     (internal rows, walks, reached leaves, leaf draws), projecting every row
     with the fused head then the tree verifier on its bf16 logits, and the
     library GEMM then the same verifier.  Every variant draws each request's
-    uniforms from its own generator, as the reference does."""
+    uniforms from its own generator, and runs with validate=False, as the
+    reference decoder calls its verifiers
+    (continuous_tree_block_decode.py:1869-2045)."""
     from specgrove_amd import verify
     vocab = weight.shape[0]
     tokens = [[int(t) % vocab for t in ts] for ts in wl.tokens]
@@ -450,17 +452,17 @@ def verify_wave_bench(torch, np, W, ops, wl, hidden, weight, device, iters=5):
 
     def lazy():
         verify.tree_verify_hip_lazy_projection_batched(wl.parents, tokens, hidden, weight,
-                                                       generators=generators)
+                                                       generators=generators, validate=False)
 
     def fused_full():
         logits = ops.lm_head(hidden, weight).logits[:, :vocab]
         verify.tree_verify_hip_rejection_batched(wl.parents, tokens, logits,
-                                                 generators=generators)
+                                                 generators=generators, validate=False)
 
     def library_full():
         logits = torch.matmul(hidden, weight.T)
         verify.tree_verify_hip_rejection_batched(wl.parents, tokens, logits,
-                                                 generators=generators)
+                                                 generators=generators, validate=False)
 
     out = {"requests": count, "rows": wl.total_rows}
     for name, fn in (("lazy_projection_us", lazy), ("every_row_fused_head_us", fused_full),
