@@ -24,6 +24,7 @@ Differences, by design:
 """
 from __future__ import annotations
 
+import itertools
 import math
 from typing import Sequence
 
@@ -222,11 +223,12 @@ def _lazy_meta(parents_batch, tokens_batch):
     total = sum(rows)
     row_offset = np.zeros(count + 1, np.int32)
     np.cumsum(rows, out=row_offset[1:])
-    parent = np.concatenate([np.asarray(p, np.int32).reshape(-1) for p in parents_batch])
-    token = np.concatenate([np.asarray([-1] + list(t), np.int32).reshape(-1)
-                            for t in tokens_batch])
-    if parent.size != total or token.size != total:
+    if sum(len(t) for t in tokens_batch) != total - count:
         raise ValueError("not a batch of trees")
+    # One pass over the Python lists each (int32 range enforced by fromiter).
+    parent = np.fromiter(itertools.chain.from_iterable(parents_batch), np.int32, total)
+    token = np.fromiter(itertools.chain.from_iterable(
+        itertools.chain((-1,), t) for t in tokens_batch), np.int32, total)
     owner = np.repeat(np.arange(count, dtype=np.int32), rows)
     local = np.arange(total, dtype=np.int32) - row_offset[owner]
     edge = (parent >= 0) & (parent < local)
