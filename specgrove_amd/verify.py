@@ -273,13 +273,13 @@ def tree_verify_hip_lazy_projection_batched(parents_batch: Sequence[Sequence[int
     if probability_dtype != torch.float32:
         raise ValueError("The HIP lazy projection uses fp32 probability arithmetic")
     weight = _head_weight(lm_head)
-    # The internal-row projection is started before the host-side validation
-    # below, so that the two overlap.  Its row indices come from the
-    # unvalidated parents (non-edges skipped, every index in range; the kernel
-    # also bounds-checks each one); an invalid call then raises below, with
-    # the same errors in the same order, before anything is sampled.
-    # The metadata goes to the device first (a synchronous copy, while the GPU
-    # has nothing of this call queued).
+    # The wave's metadata is copied to the device (a synchronous copy, while
+    # nothing of this call is queued yet) and the internal-row projection is
+    # started before the host-side validation below, so that the two overlap.
+    # The row indices come from the unvalidated parents (non-edges skipped,
+    # every index in range; the kernel also bounds-checks each one); an
+    # invalid call then raises below, with the same errors in the same order,
+    # before anything is sampled.
     early, early_meta, early_head = None, None, None
     try:
         early_hidden = _lazy_hidden(final_hidden, count, [len(p) for p in parents_batch], weight)
