@@ -409,17 +409,22 @@ def lm_head_bench(torch, np, W, ops, device, iters=10, warmup=2):
     out = {"workload": f"{wl.name}: H {hidden_size}, V {vocab}, bf16 weight "
                        f"{vocab * hidden_size * 2 / 1e9:.3f} GB",
            "total_rows": wl.total_rows, "internal_rows": int(internal.size)}
+    # The head's weight packed once (as at model load) for sg_lm_head_packed.
+    packed = ops.pack_lm_head(weight)
     for name, rows in (("internal", internal), ("leaf_pass", leaves),
                        ("every_row", np.arange(wl.total_rows, dtype=np.int32))):
         index = torch.from_numpy(rows).to(device)
         for _ in range(warmup):
             ops.lm_head(hidden, weight, index)
+            ops.lm_head(hidden, packed, index)
         torch.cuda.synchronize()
         ms = back_to_back(torch, lambda k: ops.lm_head(hidden, weight, index), iters)
+        ms_packed = back_to_back(torch, lambda k: ops.lm_head(hidden, packed, index), iters)
         flops = 2.0 * rows.size * hidden_size * vocab
         line = {"rows": int(rows.size), "us_back_to_back": ms * 1e3,
                 "tflops": flops / (ms * 1e-3) / 1e12,
-                "frac": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS}
+                "frac": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+                "packed_weight_us_back_to_back": ms_packed * 1e3}
         if name == "internal":
             sel = hidden[index.long()].contiguous()
             logits = torch.empty((rows.size, vocab), dtype=torch.bfloat16, device=device)
@@ -431,14 +436,17 @@ def lm_head_bench(torch, np, W, ops, device, iters=10, warmup=2):
             line["library_gemm_us"] = gemm * 1e3
             line["library_gemm_plus_stats_us"] = (gemm + stats) * 1e3
         out[name] = line
-    out["verify_wave"] = verify_wave_bench(torch, np, W, ops, wl, hidden, weight, device)
+    out["verify_wave"] = verify_wave_bench(torch, np, W, ops, wl, hidden, weight, device,
+                                           packed=packed)
+    del packed
     return out
 
 
-def verify_wave_bench(torch, np, W, ops, wl, hidden, weight, device, iters=5):
+def verify_wave_bench(torch, np, W, ops, wl, hidden, weight, device, iters=5, packed=None):
     """Wall time per wave of the whole verification from the final hidden
     rows (host transfers between the passes included): the lazy projection
-    (internal rows, walks, reached leaves, leaf draws), projecting every row
+    (internal rows, walks, reached leaves, leaf draws; with the plain and,
+    when given, the packed head weight), projecting every row
     with the fused head then the tree verifier on its bf16 logits, and the
     library GEMM then the same verifier.  Every variant draws each request's
     uniforms from its own generator, and runs with validate=False, as the
@@ -454,6 +462,10 @@ def verify_wave_bench(torch, np, W, ops, wl, hidden, weight, device, iters=5):
         verify.tree_verify_hip_lazy_projection_batched(wl.parents, tokens, hidden, weight,
                                                        generators=generators, validate=False)
 
+    def lazy_packed():
+        verify.tree_verify_hip_lazy_projection_batched(wl.parents, tokens, hidden, packed,
+                                                       generators=generators, validate=False)
+
     def fused_full():
         logits = ops.lm_head(hidden, weight).logits[:, :vocab]
         verify.tree_verify_hip_rejection_batched(wl.parents, tokens, logits,
@@ -465,8 +477,11 @@ def verify_wave_bench(torch, np, W, ops, wl, hidden, weight, device, iters=5):
                                                  generators=generators, validate=False)
 
     out = {"requests": count, "rows": wl.total_rows}
-    for name, fn in (("lazy_projection_us", lazy), ("every_row_fused_head_us", fused_full),
-                     ("every_row_library_gemm_us", library_full)):
+    variants = [("lazy_projection_us", lazy), ("every_row_fused_head_us", fused_full),
+                ("every_row_library_gemm_us", library_full)]
+    if packed is not None:
+        variants.insert(1, ("lazy_projection_packed_head_us", lazy_packed))
+    for name, fn in variants:
         fn()
         torch.cuda.synchronize()
         with gc_paused():

@@ -136,7 +136,8 @@ EXPORTED_SYMBOLS = (
     "sg_tree_attn_plan", "sg_tree_attn_fwd", "sg_kv_commit",
     "sg_tree_sample", "sg_tree_sample_workspace_bytes", "sg_row_stats", "sg_exp_probe",
     "sg_tree_sample_noalloc", "sg_tree_attn_plan_check", "sg_kv_split",
-    "sg_lm_head", "sg_lm_head_tile_count",
+    "sg_lm_head", "sg_lm_head_tile_count", "sg_lm_head_packed", "sg_lm_head_pack_weight",
+    "sg_lm_head_packed_bytes",
     "sg_add_rmsnorm", "sg_qk_norm_rope", "sg_silu_mul", "sg_gather_rows",
 )
 
@@ -193,6 +194,12 @@ def load() -> ctypes.CDLL:
     lib.sg_lm_head.argtypes = [ctypes.POINTER(SgLmHeadArgs), c_void_p]
     lib.sg_lm_head_tile_count.restype = c_i64
     lib.sg_lm_head_tile_count.argtypes = [c_i32]
+    lib.sg_lm_head_packed.restype = c_i32
+    lib.sg_lm_head_packed.argtypes = [ctypes.POINTER(SgLmHeadArgs), c_void_p]
+    lib.sg_lm_head_pack_weight.restype = c_i32
+    lib.sg_lm_head_pack_weight.argtypes = [c_void_p, c_i64, c_i32, c_i32, c_void_p, c_void_p]
+    lib.sg_lm_head_packed_bytes.restype = c_i64
+    lib.sg_lm_head_packed_bytes.argtypes = [c_i32, c_i32]
     lib.sg_add_rmsnorm.restype = c_i32
     lib.sg_add_rmsnorm.argtypes = [ctypes.POINTER(SgAddRmsNormArgs), c_void_p]
     lib.sg_qk_norm_rope.restype = c_i32

@@ -128,7 +128,12 @@ __device__ __forceinline__ bool tile_of(int b, int v_tiles, int r_tiles, int& vt
   return vt < v_tiles;
 }
 
-template <int R>
+// kPacked: the weight is in the packed layout of sg_lm_head_pack_weight
+// (tile, 32-dim stage, 256 rows x 32 dims): every stage of a tile is 16 KiB
+// contiguous and every copy a contiguous 1 KiB.  Otherwise the weight is
+// row-major [V, weight_row_stride] and a copy reads 64 bytes of each of 16
+// rows.  The arithmetic is the same, so are the results.
+template <int R, bool kPacked>
 __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_kernel(
     SgLmHeadArgs a, int v_tiles, int r_tiles) {
   using T = RowTile<R>;
@@ -154,8 +159,13 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
   // bytes and four lanes one row's 64 bytes: every copy touches 16 cache
   // lines instead of 32.
   uint32_t w_off[4], w_lds[4], x_off[R], x_lds[R];
+  const int steps = a.hidden_size / kStepK;
   const unsigned char* wbase =
-      static_cast<const unsigned char*>(a.weight_dev) + static_cast<int64_t>(v0) * a.weight_row_stride * 2;
+      static_cast<const unsigned char*>(a.weight_dev) +
+      (kPacked ? static_cast<int64_t>(vt) * steps * kWBytes
+               : static_cast<int64_t>(v0) * a.weight_row_stride * 2);
+  // Bytes between a tile's consecutive stages.
+  constexpr int64_t kWStep = kPacked ? kWBytes : kStepK * 2;
   const unsigned char* xbase = static_cast<const unsigned char*>(a.hidden_dev);
   bool bad_index = false;
   // Copy q moves rows 16q .. 16q+15 of an operand, 64 bytes (the stage's 32
@@ -170,7 +180,9 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
     // Tokens past the vocabulary re-read the last token (finite data the
     // epilogue drops).
     const int tok = min(v0 + row, V - 1) - v0;
-    w_off[i] = static_cast<uint32_t>((static_cast<int64_t>(tok) * a.weight_row_stride + dim) * 2);
+    w_off[i] = kPacked ? static_cast<uint32_t>(row * kStepK * 2 + dim * 2)
+                       : static_cast<uint32_t>((static_cast<int64_t>(tok) * a.weight_row_stride +
+                                                dim) * 2);
     w_lds[i] = static_cast<uint32_t>(1024 * q);
   }
 #pragma unroll
@@ -191,10 +203,9 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
   if (bad_index && a.status_dev != nullptr) atomicExch(a.status_dev, SG_EINVAL);
 
   const uint32_t ring = lds_addr(smem);
-  const int steps = a.hidden_size / kStepK;
   auto issue = [&](int s) {
     const uint32_t stage = ring + (s % kLmStages) * T::kStage;
-    const unsigned char* wk = wbase + static_cast<int64_t>(s) * kStepK * 2;
+    const unsigned char* wk = wbase + static_cast<int64_t>(s) * kWStep;
     const unsigned char* xk = xbase + static_cast<int64_t>(s) * kStepK * 2;
 #pragma unroll
     for (int i = 0; i < 4; ++i) dma16(wk, w_off[i], stage + w_lds[i]);
@@ -276,7 +287,7 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
     const bool refill = s + kLmStages - 1 < steps;
     const int t = s + kLmStages - 1;
     const uint32_t stage_t = ring + (t % kLmStages) * T::kStage;
-    const unsigned char* wk = wbase + static_cast<int64_t>(t) * kStepK * 2;
+    const unsigned char* wk = wbase + static_cast<int64_t>(t) * kWStep;
     const unsigned char* xk = xbase + static_cast<int64_t>(t) * kStepK * 2;
     const unsigned char* st = smem + (s % kLmStages) * T::kStage;
     constexpr int nd = 4 + R;
@@ -440,6 +451,83 @@ __global__ __launch_bounds__(kMergeRowsPerBlock * kWave) void lm_head_rows_kerne
   }
 }
 
+// One 16 KiB stage of the packed weight per workgroup: packed stage
+// (vt, s) row r dim d = weight[256 vt + r][32 s + d], zero for rows >= V.
+// Thread t moves four 16-byte chunks: chunk c = t + 256 k is row c / 4,
+// dims 8 (c % 4) .. +7.
+__global__ __launch_bounds__(256) void lm_head_pack_kernel(const uint16_t* __restrict__ weight,
+                                                           int64_t row_stride, int vocab,
+                                                           int steps, uint16_t* __restrict__ packed) {
+  const int vt = blockIdx.x / steps;
+  const int s = blockIdx.x % steps;
+  uint4* dst = reinterpret_cast<uint4*>(packed + static_cast<int64_t>(blockIdx.x) * kTileV * kStepK);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int c = threadIdx.x + 256 * k;
+    const int row = kTileV * vt + c / 4;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (row < vocab)
+      v = *reinterpret_cast<const uint4*>(weight + static_cast<int64_t>(row) * row_stride +
+                                          kStepK * s + 8 * (c % 4));
+    dst[c] = v;
+  }
+}
+
+// Checks shared by both weight layouts; v_tiles and the launch follow.
+int check_lm_head(const SgLmHeadArgs& a, bool packed) {
+  SG_REQUIRE(a.num_hidden_rows >= 1, "num_hidden_rows must be positive");
+  SG_REQUIRE(a.row_index_dev != nullptr || a.num_hidden_rows >= a.num_rows,
+             "without a row index the hidden rows must cover every projected row");
+  SG_REQUIRE(a.hidden_dev && a.weight_dev && a.logits_dev && a.tile_stats_dev &&
+                 a.row_max_dev && a.row_sum_dev,
+             "null device pointer");
+  SG_REQUIRE(a.hidden_row_stride >= a.hidden_size &&
+                 (packed || a.weight_row_stride >= a.hidden_size) &&
+                 a.logits_row_stride >= a.vocab,
+             "row strides must cover the rows");
+  SG_REQUIRE((a.hidden_row_stride | (packed ? 0 : a.weight_row_stride) | a.logits_row_stride) %
+                     8 == 0,
+             "row strides must be multiples of 8 elements");
+  SG_REQUIRE((reinterpret_cast<uintptr_t>(a.hidden_dev) | reinterpret_cast<uintptr_t>(a.weight_dev) |
+              reinterpret_cast<uintptr_t>(a.logits_dev)) % 16 == 0,
+             "hidden, weight and logits must be 16-byte aligned");
+  // The per-lane copy offsets are 32-bit: a tile's weight rows and the whole
+  // hidden matrix must each stay below 4 GiB.
+  SG_REQUIRE(packed || static_cast<int64_t>(kTileV) * a.weight_row_stride * 2 < (int64_t{1} << 32),
+             "weight rows too long");
+  SG_REQUIRE(static_cast<int64_t>(a.num_hidden_rows) * a.hidden_row_stride * 2 < (int64_t{1} << 32),
+             "hidden matrix above 4 GiB");
+  return SG_OK;
+}
+
+int launch_lm_head(const SgLmHeadArgs& a, bool packed, hipStream_t s) {
+  const int v_tiles = (a.vocab + kTileV - 1) / kTileV;
+  auto launch = [&](auto tag) -> int {
+    constexpr int R = decltype(tag)::value;
+    const int r_tiles = (a.num_rows + RowTile<R>::kRows - 1) / RowTile<R>::kRows;
+    const int64_t blocks =
+        static_cast<int64_t>((v_tiles + kLmXcds - 1) / kLmXcds) * kLmXcds * r_tiles;
+    SG_REQUIRE(blocks < INT32_MAX, "wave too large");
+    if (packed) {
+      lm_head_kernel<R, true><<<dim3(static_cast<unsigned>(blocks)), dim3(kLmThreads), 0, s>>>(
+          a, v_tiles, r_tiles);
+    } else {
+      lm_head_kernel<R, false><<<dim3(static_cast<unsigned>(blocks)), dim3(kLmThreads), 0, s>>>(
+          a, v_tiles, r_tiles);
+    }
+    SG_LAUNCH_CHECK();
+    return SG_OK;
+  };
+  const int rc = a.num_rows <= 64    ? launch(std::integral_constant<int, 1>{})
+                 : a.num_rows <= 128 ? launch(std::integral_constant<int, 2>{})
+                                     : launch(std::integral_constant<int, 4>{});
+  if (rc != SG_OK) return rc;
+  const int merge_blocks = (a.num_rows + kMergeRowsPerBlock - 1) / kMergeRowsPerBlock;
+  lm_head_rows_kernel<<<dim3(merge_blocks), dim3(kMergeRowsPerBlock * kWave), 0, s>>>(a);
+  SG_LAUNCH_CHECK();
+  return SG_OK;
+}
+
 }  // namespace
 }  // namespace sg
 
@@ -457,45 +545,53 @@ extern "C" int sg_lm_head(const SgLmHeadArgs* args, sg_stream_t stream) {
   SG_REQUIRE(a.hidden_size >= 2 * kStepK && a.hidden_size % (2 * kStepK) == 0,
              "hidden_size must be a positive multiple of 64");
   if (a.num_rows == 0) return SG_OK;
-  SG_REQUIRE(a.num_hidden_rows >= 1, "num_hidden_rows must be positive");
-  SG_REQUIRE(a.row_index_dev != nullptr || a.num_hidden_rows >= a.num_rows,
-             "without a row index the hidden rows must cover every projected row");
-  SG_REQUIRE(a.hidden_dev && a.weight_dev && a.logits_dev && a.tile_stats_dev &&
-                 a.row_max_dev && a.row_sum_dev,
-             "null device pointer");
-  SG_REQUIRE(a.hidden_row_stride >= a.hidden_size && a.weight_row_stride >= a.hidden_size &&
-                 a.logits_row_stride >= a.vocab,
-             "row strides must cover the rows");
-  SG_REQUIRE((a.hidden_row_stride | a.weight_row_stride | a.logits_row_stride) % 8 == 0,
-             "row strides must be multiples of 8 elements");
-  SG_REQUIRE((reinterpret_cast<uintptr_t>(a.hidden_dev) | reinterpret_cast<uintptr_t>(a.weight_dev) |
-              reinterpret_cast<uintptr_t>(a.logits_dev)) % 16 == 0,
-             "hidden, weight and logits must be 16-byte aligned");
-  // The per-lane copy offsets are 32-bit: a tile's weight rows and the whole
-  // hidden matrix must each stay below 4 GiB.
-  SG_REQUIRE(static_cast<int64_t>(kTileV) * a.weight_row_stride * 2 < (int64_t{1} << 32),
-             "weight rows too long");
-  SG_REQUIRE(static_cast<int64_t>(a.num_hidden_rows) * a.hidden_row_stride * 2 < (int64_t{1} << 32),
-             "hidden matrix above 4 GiB");
-  const int v_tiles = (a.vocab + kTileV - 1) / kTileV;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  auto launch = [&](auto tag) -> int {
-    constexpr int R = decltype(tag)::value;
-    const int r_tiles = (a.num_rows + RowTile<R>::kRows - 1) / RowTile<R>::kRows;
-    const int64_t blocks =
-        static_cast<int64_t>((v_tiles + kLmXcds - 1) / kLmXcds) * kLmXcds * r_tiles;
-    SG_REQUIRE(blocks < INT32_MAX, "wave too large");
-    lm_head_kernel<R><<<dim3(static_cast<unsigned>(blocks)), dim3(kLmThreads), 0, s>>>(
-        a, v_tiles, r_tiles);
-    SG_LAUNCH_CHECK();
-    return SG_OK;
-  };
-  const int rc = a.num_rows <= 64    ? launch(std::integral_constant<int, 1>{})
-                 : a.num_rows <= 128 ? launch(std::integral_constant<int, 2>{})
-                                     : launch(std::integral_constant<int, 4>{});
+  const int rc = check_lm_head(a, false);
   if (rc != SG_OK) return rc;
-  const int merge_blocks = (a.num_rows + kMergeRowsPerBlock - 1) / kMergeRowsPerBlock;
-  lm_head_rows_kernel<<<dim3(merge_blocks), dim3(kMergeRowsPerBlock * kWave), 0, s>>>(a);
+  return launch_lm_head(a, false, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t sg_lm_head_packed_bytes(int32_t vocab, int32_t hidden_size) {
+  using namespace sg;
+  if (vocab < 1 || hidden_size < 2 * kStepK || hidden_size % (2 * kStepK) != 0) return -1;
+  return static_cast<int64_t>((vocab + kTileV - 1) / kTileV) * kTileV * hidden_size * 2;
+}
+
+extern "C" int sg_lm_head_pack_weight(const void* weight_dev, int64_t weight_row_stride,
+                                      int32_t vocab, int32_t hidden_size, void* packed_dev,
+                                      sg_stream_t stream) {
+  using namespace sg;
+  clear_error();
+  SG_REQUIRE(vocab >= 1, "vocab must be positive");
+  SG_REQUIRE(hidden_size >= 2 * kStepK && hidden_size % (2 * kStepK) == 0,
+             "hidden_size must be a positive multiple of 64");
+  SG_REQUIRE(weight_dev && packed_dev, "null device pointer");
+  SG_REQUIRE(weight_row_stride >= hidden_size && weight_row_stride % 8 == 0,
+             "weight_row_stride must cover the row and be a multiple of 8 elements");
+  SG_REQUIRE((reinterpret_cast<uintptr_t>(weight_dev) | reinterpret_cast<uintptr_t>(packed_dev)) %
+                     16 == 0,
+             "weight and packed must be 16-byte aligned");
+  const int steps = hidden_size / kStepK;
+  const int64_t blocks = static_cast<int64_t>((vocab + kTileV - 1) / kTileV) * steps;
+  SG_REQUIRE(blocks < INT32_MAX, "weight too large");
+  lm_head_pack_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                        static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint16_t*>(weight_dev), weight_row_stride, vocab, steps,
+      static_cast<uint16_t*>(packed_dev));
   SG_LAUNCH_CHECK();
   return SG_OK;
+}
+
+extern "C" int sg_lm_head_packed(const SgLmHeadArgs* args, sg_stream_t stream) {
+  using namespace sg;
+  clear_error();
+  SG_REQUIRE(args != nullptr, "null args");
+  const SgLmHeadArgs& a = *args;
+  SG_REQUIRE(a.num_rows >= 0, "num_rows must be non-negative");
+  SG_REQUIRE(a.vocab >= 1, "vocab must be positive");
+  SG_REQUIRE(a.hidden_size >= 2 * kStepK && a.hidden_size % (2 * kStepK) == 0,
+             "hidden_size must be a positive multiple of 64");
+  if (a.num_rows == 0) return SG_OK;
+  const int rc = check_lm_head(a, true);
+  if (rc != SG_OK) return rc;
+  return launch_lm_head(a, true, static_cast<hipStream_t>(stream));
 }

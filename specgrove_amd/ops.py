@@ -641,18 +641,51 @@ class LmHeadResult:
     status: torch.Tensor      # [1] i32: SG_EINVAL when a row index was out of range
 
 
-def lm_head(hidden: torch.Tensor, weight: torch.Tensor,
+class PackedLmHead:
+    """``lm_head.weight`` re-laid out once for ``sg_lm_head_packed`` (every
+    16 KiB weight stage of the kernel contiguous).  Holds the packed bytes
+    beside the model's own weight; ``shape`` and ``dtype`` are the original
+    weight's, so it stands in for it wherever ``lm_head`` takes a weight."""
+    __slots__ = ("packed", "shape", "dtype", "device")
+
+    def __init__(self, weight: torch.Tensor):
+        _check_device_tensor(weight, "weight", torch.bfloat16)
+        _require(weight.dim() == 2 and weight.stride(1) == 1,
+                 "weight must be a row-contiguous matrix")
+        vocab, hsize = weight.shape
+        lib = _lib.load()
+        nbytes = int(lib.sg_lm_head_packed_bytes(vocab, hsize))
+        _require(nbytes > 0, "weight size unsupported (H a positive multiple of 64)")
+        self.packed = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=weight.device)
+        _lib.check(lib.sg_lm_head_pack_weight(weight.data_ptr(), weight.stride(0), vocab, hsize,
+                                              self.packed.data_ptr(), _stream_handle()),
+                   "sg_lm_head_pack_weight")
+        self.shape = torch.Size((vocab, hsize))
+        self.dtype = weight.dtype
+        self.device = weight.device
+
+
+def pack_lm_head(weight: torch.Tensor) -> PackedLmHead:
+    """One-time packing of ``lm_head.weight`` for ``lm_head`` (enqueued on
+    torch's current stream)."""
+    return PackedLmHead(weight)
+
+
+def lm_head(hidden: torch.Tensor, weight,
             row_index: torch.Tensor | None = None) -> LmHeadResult:
     """bf16 logits of the selected hidden rows and their softmax statistics
-    (sg_lm_head).
+    (sg_lm_head, or sg_lm_head_packed for a PackedLmHead).
 
     ``hidden`` [N, H] bf16 (row-contiguous, H a multiple of 64), ``weight``
-    [V, H] bf16 (``lm_head.weight``), ``row_index`` [Rp] i32 selects the rows
+    [V, H] bf16 (``lm_head.weight``) or its ``PackedLmHead`` (same results,
+    bit for bit), ``row_index`` [Rp] i32 selects the rows
     to project (None: all N).  Replaces ``lm_head(hidden)`` +
     ``probabilities(...)`` on the rows a tree walk can need
     (fused_tree_sampling.py:2899-2913, :2974-2984).
     """
-    for t, name in ((hidden, "hidden"), (weight, "weight")):
+    packed = isinstance(weight, PackedLmHead)
+    checked = (hidden,) if packed else (hidden, weight)
+    for t, name in zip(checked, ("hidden", "weight")):
         _check_device_tensor(t, name, torch.bfloat16)
         _require(t.dim() == 2 and t.stride(1) == 1, f"{name} must be a row-contiguous matrix")
     _require(hidden.shape[1] == weight.shape[1], "hidden and weight disagree on the hidden size")
@@ -679,13 +712,14 @@ def lm_head(hidden: torch.Tensor, weight: torch.Tensor,
     a.hidden_dev = hidden.data_ptr()
     a.hidden_row_stride = hidden.stride(0)
     a.row_index_dev = row_index.data_ptr() if row_index is not None else 0
-    a.weight_dev = weight.data_ptr()
-    a.weight_row_stride = weight.stride(0)
+    a.weight_dev = weight.packed.data_ptr() if packed else weight.data_ptr()
+    a.weight_row_stride = hsize if packed else weight.stride(0)
     a.logits_dev = logits.data_ptr()
     a.logits_row_stride = pad
     a.tile_stats_dev = res.tile_stats.data_ptr()
     a.row_max_dev = res.row_max.data_ptr()
     a.row_sum_dev = res.row_sum.data_ptr()
     a.status_dev = res.status.data_ptr()
-    _lib.check(_lib.load().sg_lm_head(ctypes.byref(a), _stream_handle()), "sg_lm_head")
+    name = "sg_lm_head_packed" if packed else "sg_lm_head"
+    _lib.check(getattr(_lib.load(), name)(ctypes.byref(a), _stream_handle()), name)
     return res

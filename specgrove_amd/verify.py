@@ -175,9 +175,11 @@ def tree_verify_hip_rejection(parents, tokens, all_logits: torch.Tensor,
 LAZY_VERIFIER_NAME = "hip_lazy_projection"
 
 
-def _head_weight(lm_head) -> torch.Tensor:
-    """The [V, H] bf16 weight of an ``nn.Linear`` vocabulary head (no bias) or
-    the weight tensor itself."""
+def _head_weight(lm_head):
+    """The [V, H] bf16 weight of an ``nn.Linear`` vocabulary head (no bias),
+    the weight tensor itself, or its ``ops.PackedLmHead`` (used as it is)."""
+    if isinstance(lm_head, ops.PackedLmHead):
+        return lm_head
     weight = getattr(lm_head, "weight", lm_head)
     if getattr(lm_head, "bias", None) is not None:
         raise ValueError("The HIP lazy projection supports a vocabulary head without bias")
@@ -259,7 +261,8 @@ def tree_verify_hip_lazy_projection_batched(parents_batch: Sequence[Sequence[int
 
     ``final_hidden`` is ``[B, N, H]`` (equal trees, as the reference) or the
     packed wave ``[R, H]`` / ``[1, R, H]``; ``lm_head`` an ``nn.Linear``
-    without bias (or its bf16 ``[V, H]`` weight).  Returns, per request,
+    without bias, its bf16 ``[V, H]`` weight, or that weight packed once by
+    ``ops.pack_lm_head`` (same results, faster weight reads).  Returns, per request,
     ``(nodes, tokens, bonus, stats)`` with the reference's projection counts.
     """
     count = len(parents_batch)

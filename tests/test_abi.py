@@ -233,6 +233,35 @@ def test_lm_head_and_projected_sampler_reject_bad_arguments_on_the_host():
     assert lib.sg_tree_sample(ctypes.byref(s), None) == _lib.SG_EINVAL
 
 
+def test_packed_lm_head_rejects_bad_arguments_on_the_host():
+    lib = _lib.load()
+    assert lib.sg_lm_head_packed_bytes(151936, 4096) == 594 * 256 * 4096 * 2
+    assert lib.sg_lm_head_packed_bytes(300, 128) == 2 * 256 * 128 * 2
+    for vocab, hsize in ((0, 4096), (100, 4000), (100, 32)):
+        assert lib.sg_lm_head_packed_bytes(vocab, hsize) == -1
+    for args, text in (((0x1000, 4096, 0, 4096, 0x2000), b"vocab"),
+                       ((0x1000, 4096, 100, 4000, 0x2000), b"multiple of 64"),
+                       ((0, 4096, 100, 4096, 0x2000), b"null"),
+                       ((0x1000, 4000, 100, 4096, 0x2000), b"weight_row_stride"),
+                       ((0x1000, 4100, 100, 4096, 0x2000), b"weight_row_stride"),
+                       ((0x1008, 4096, 100, 4096, 0x2000), b"aligned")):
+        assert lib.sg_lm_head_pack_weight(*args, None) == _lib.SG_EINVAL, args
+        assert text in lib.sg_last_error(), (args, lib.sg_last_error())
+    a = _lib.SgLmHeadArgs()
+    a.num_rows, a.hidden_size, a.vocab, a.num_hidden_rows = 4, 4096, 151936, 4
+    for name in ("hidden_dev", "weight_dev", "logits_dev", "tile_stats_dev", "row_max_dev",
+                 "row_sum_dev"):
+        setattr(a, name, 0x1000)
+    a.hidden_row_stride, a.weight_row_stride, a.logits_row_stride = 4096, 0, 151936
+    a.hidden_size = 4000
+    assert lib.sg_lm_head_packed(ctypes.byref(a), None) == _lib.SG_EINVAL
+    a.hidden_size, a.weight_dev = 4096, 0
+    assert lib.sg_lm_head_packed(ctypes.byref(a), None) == _lib.SG_EINVAL
+    assert b"null" in lib.sg_last_error()
+    a.num_rows = 0
+    assert lib.sg_lm_head_packed(ctypes.byref(a), None) == _lib.SG_OK
+
+
 def test_layer_ops_reject_bad_arguments_on_the_host():
     """The decoder-stack kernels check shapes, strides and 16-byte alignment
     before any launch (fake, never-dereferenced device addresses)."""

@@ -196,3 +196,50 @@ def test_lazy_projection_rejects_bad_calls_after_starting_the_projection(device)
     lazy = verify.tree_verify_hip_lazy_projection_batched(parents, tokens, hidden, weight,
                                                           generators=gens)
     assert len(lazy) == len(sizes)
+
+
+def test_packed_weight_layout(device):
+    """sg_lm_head_pack_weight: tile t, stage s holds rows 256t.. x dims 32s..,
+    row-major, zero past the vocabulary (checked against a host re-layout)."""
+    g = torch.Generator(device="cpu").manual_seed(11)
+    vocab, hsize = 300, 128
+    w = (torch.randn(vocab, hsize + 8, generator=g) * 0.1).to(torch.bfloat16)[:, :hsize]
+    packed = ops.pack_lm_head(w.to(device))
+    torch.cuda.synchronize()
+    tiles, steps = (vocab + 255) // 256, hsize // 32
+    padded = torch.zeros(tiles * 256, hsize, dtype=torch.bfloat16)
+    padded[:vocab] = w
+    want = padded.view(tiles, 256, steps, 32).permute(0, 2, 1, 3).reshape(-1)
+    assert packed.shape == (vocab, hsize)
+    assert torch.equal(packed.packed.cpu(), want)
+
+
+@pytest.mark.parametrize("rows", [40, 64, 130, 300])
+@pytest.mark.parametrize("vocab", [151936, 1000])
+def test_packed_lm_head_equals_row_major(device, rows, vocab):
+    """The packed-weight kernel gives the row-major kernel's outputs bit for bit."""
+    g = torch.Generator(device=device).manual_seed(rows + vocab)
+    hidden = (torch.randn(512, 512, device=device, generator=g)).to(torch.bfloat16)
+    weight = (torch.randn(vocab, 512, device=device, generator=g) * 0.05).to(torch.bfloat16)
+    index = torch.randperm(512, device=device, generator=g)[:rows].to(torch.int32)
+    plain = ops.lm_head(hidden, weight, index)
+    packed = ops.lm_head(hidden, ops.pack_lm_head(weight), index)
+    torch.cuda.synchronize()
+    assert torch.equal(plain.logits, packed.logits)
+    for name in ("tile_stats", "row_max", "row_sum", "status"):
+        assert torch.equal(getattr(plain, name), getattr(packed, name)), name
+
+
+def test_lazy_projection_with_packed_head(device):
+    """The lazy verifier given the packed head decides exactly as with the
+    plain weight."""
+    sizes = [1, 9, 16, 3, 24, 7]
+    parents, tokens, hidden, weight = _wave(device, 3, sizes)
+    gens = lambda: [torch.Generator(device=device).manual_seed(300 + i)  # noqa: E731
+                    for i in range(len(sizes))]
+    plain = verify.tree_verify_hip_lazy_projection_batched(parents, tokens, hidden, weight,
+                                                           generators=gens())
+    packed = verify.tree_verify_hip_lazy_projection_batched(parents, tokens, hidden,
+                                                            ops.pack_lm_head(weight),
+                                                            generators=gens())
+    assert [r[:3] for r in plain] == [r[:3] for r in packed]
