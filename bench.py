@@ -280,10 +280,14 @@ def commit_all_layers(torch, np, ops, wl, meta, device, layers=36, iters=50, war
     return {"layers": layers, "us_per_call": us, "rows_per_layer": rows,
             "gbs": 2 * rows * hkv * d * 2 * 2 * layers / (us * 1e-6) / 1e9}
 
-def sampler_bench(torch, W, ops, device, iters, warmup):
+def sampler_bench(torch, W, ops, device, iters, warmup, dtype=None):
+    """The 64 x 32 x 151936 tree-sampling call over N_SETS rotating logits
+    sets (fp32, or rounded to ``dtype``): per-call and back-to-back times."""
     sets = []
     for s in range(N_SETS):
         wl, logits, uniforms = W.sampler_workload(device, seed=200 + s)
+        if dtype is not None:
+            logits = logits.to(dtype)
         parent, token = wl.flat_parent_token()
         sets.append(dict(wl=wl, logits=logits, uniforms=uniforms,
                          row_offset=torch.from_numpy(wl.row_offset).to(device),
@@ -821,6 +825,22 @@ def main():
             "gbs": sbytes / (samp_b2b * 1e-3) / 1e9,
             "frac": sbytes / (samp_b2b * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "algorithmic_bytes": sbytes,
+        }
+        # The same call on bf16 logits (what the LM head writes): half the
+        # bytes, the same decisions as on their fp32 widening.
+        _, bf_ms, bf_sets, bf_b2b = sampler_bench(torch, W, ops, device, steps, warmup,
+                                                  dtype=torch.bfloat16)
+        del bf_sets
+        torch.cuda.empty_cache()
+        bbytes = sbytes // 2
+        result["sampler_bf16"] = {
+            "workload": swl.name + " (bf16 logits)",
+            "us_back_to_back": bf_b2b * 1e3,
+            "us_median_per_call": statistics.median(bf_ms) * 1e3,
+            "nodes_per_s": swl.total_rows / (bf_b2b * 1e-3),
+            "gbs": bbytes / (bf_b2b * 1e-3) / 1e9,
+            "frac": bbytes / (bf_b2b * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "algorithmic_bytes": bbytes,
         }
     if not args.no_lm_head:
         torch.cuda.empty_cache()
