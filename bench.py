@@ -76,9 +76,10 @@ def parse_args():
                         "calibrate FETCH_SIZE / WRITE_SIZE; prints nothing")
     p.add_argument("--counters-workload", default="qwen3_8b",
                    choices=["qwen3_8b", "qwen3_4b", "tier128", "long_context", "lm_head",
-                            "layer"],
+                            "layer", "sampler"],
                    help="what a --counters-only run repeats: an attention wave, the LM "
-                        "head over the Qwen3-8B wave's internal rows, or one decoder layer")
+                        "head over the Qwen3-8B wave's internal rows, one decoder layer, "
+                        "or the 64 x 32 x 151936 tree-sampling call")
     return p.parse_args()
 
 
@@ -663,8 +664,8 @@ def read_traffic():
 
 
 def counters_only(torch, np, W, ops, device, steps, warmup, workload="qwen3_8b"):
-    """Attention calls (or LM head / decoder layer calls) plus a copy of known
-    size, for rocprofv3 --pmc runs."""
+    """Attention calls (or LM head, decoder layer or tree-sampling calls) plus
+    a copy of known size, for rocprofv3 --pmc runs."""
     if workload == "lm_head":
         _, hidden, weight, internal, _ = lm_head_inputs(torch, np, W, device)
         index = torch.from_numpy(internal).to(device)
@@ -674,6 +675,10 @@ def counters_only(torch, np, W, ops, device, steps, warmup, workload="qwen3_8b")
         return
     if workload == "layer":
         layer_bench(torch, np, W, ops, device, iters=steps, warmup=warmup)
+        torch.cuda.synchronize()
+        return
+    if workload == "sampler":
+        sampler_bench(torch, W, ops, device, steps, warmup)
         torch.cuda.synchronize()
         return
     make = {"qwen3_8b": W.qwen3_8b_workload, "qwen3_4b": W.qwen3_4b_workload,
