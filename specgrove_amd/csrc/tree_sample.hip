@@ -381,7 +381,7 @@ __device__ void route_request(const SgTreeSampleArgs& a, int req, int r0, int n,
   const float* __restrict__ u = a.uniforms_dev + static_cast<int64_t>(a.uniform_stride) * req;
   const int n_u = min(a.uniform_stride, 2 * kMaxTreeRows + 2);
   const int n_logits = a.num_logits_rows > 0 ? a.num_logits_rows : a.num_rows;
-  // Round 1: the tree, each node's logits row and the uniforms.
+  // First memory round trip: the tree, each node's logits row and the uniforms.
   if (tid == 0) sh.bad_rows = 0;
   for (int k = tid; k < n; k += blockDim.x) {
     sh.parent[k] = a.parent_dev[r0 + k];
@@ -390,7 +390,7 @@ __device__ void route_request(const SgTreeSampleArgs& a, int req, int r0, int n,
   }
   for (int k = tid; k < n_u; k += blockDim.x) sh.u[k] = u[k];
   __syncthreads();
-  // Round 2: the row statistics and each node's token logit in its parent's
+  // Second round trip: the row statistics and each node's token logit in its parent's
   // row (the only logits routing touches).  A node whose parent has no
   // logits row breaks the lazy-projection contract.
   for (int k = tid; k < n; k += blockDim.x) {
