@@ -16,6 +16,10 @@ TBS = code/natural/src/gbv_experiments/tree_block_skip.py):
 * ``select_ready`` (CTBD:1158-1195): continuations first, then the oldest,
   under a slot cap and a shared row budget; ages advance for the ones left
   out;
+* occupancy controls -- ``effective_row_cap`` (CTBD:1198-1216),
+  ``effective_tree_budget(s)`` (:1247-1300) and
+  ``adaptive_expansion_eligible`` (:1303-1314): larger blocks and trees
+  only when few requests are ready or active;
 * global tree budgets -- ``admit_global_proposal_states`` (CTBD:648-667),
   ``globally_feasible_budget_options`` (:670-690),
   ``active_global_tree_budget_options`` (:693-703), ``global_wave_cost``
@@ -37,7 +41,8 @@ from typing import Sequence
 
 __all__ = [
     "TreeBlock", "DraftTree", "local_tree_block", "tree_block_from_nodes", "child_for_edge",
-    "prefix_tree", "select_ready", "admit_global_proposal_states",
+    "prefix_tree", "select_ready", "effective_row_cap", "effective_tree_budget",
+    "effective_tree_budgets", "adaptive_expansion_eligible", "admit_global_proposal_states",
     "globally_feasible_budget_options", "active_global_tree_budget_options",
     "normalize_row_cost_curve", "global_wave_cost", "allocate_global_tree_budgets",
 ]
@@ -214,6 +219,69 @@ def select_ready(states: Sequence, row_cap: int, slot_capacity: int | None,
     for state in ready:
         state.age = 0 if state.request_id in picked else state.age + 1
     return chosen, blocks
+
+
+def effective_row_cap(row_cap: int, low_occupancy_row_cap: int | None,
+                      low_occupancy_threshold: int | None, ready_count: int,
+                      mid_occupancy_row_cap: int | None = None,
+                      mid_occupancy_threshold: int | None = None) -> int:
+    """Rows per request block for the next wave (CTBD:1198-1216): the
+    low-occupancy cap at or below ``low_occupancy_threshold`` ready requests,
+    else the mid-occupancy cap at or below ``mid_occupancy_threshold``, else
+    ``row_cap`` -- larger blocks only when the saved rows could not admit
+    another request anyway."""
+    if (low_occupancy_row_cap is not None and low_occupancy_threshold is not None
+            and ready_count <= low_occupancy_threshold):
+        return low_occupancy_row_cap
+    if (mid_occupancy_row_cap is not None and mid_occupancy_threshold is not None
+            and ready_count <= mid_occupancy_threshold):
+        return mid_occupancy_row_cap
+    return row_cap
+
+
+def effective_tree_budget(default_budget: int, proposal_tree_budget: int | None,
+                          low_occupancy_tree_budget: int | None,
+                          low_occupancy_tree_threshold: int | None, active_count: int) -> int:
+    """Draft-tree size at the current occupancy (CTBD:1247-1260): the
+    low-occupancy budget at or below ``low_occupancy_tree_threshold`` active
+    requests, else ``proposal_tree_budget`` or the default."""
+    if (low_occupancy_tree_budget is not None and low_occupancy_tree_threshold is not None
+            and active_count <= low_occupancy_tree_threshold):
+        return low_occupancy_tree_budget
+    return proposal_tree_budget or default_budget
+
+
+def effective_tree_budgets(states: Sequence, default_budget: int,
+                           proposal_tree_budget: int | None,
+                           low_occupancy_tree_budget: int | None,
+                           low_occupancy_tree_threshold: int | None, active_count: int,
+                           low_occupancy_expansion_slots: int | None) -> tuple[int, ...]:
+    """Per-request tree budgets (CTBD:1263-1300): when the occupancy calls
+    for the larger tree and ``low_occupancy_expansion_slots`` is below the
+    number of requests, only that many requests get it -- those with the
+    fewest generated tokens (the most remaining work), then the oldest, then
+    the lowest id; the others keep the base budget."""
+    base = proposal_tree_budget or default_budget
+    expanded = effective_tree_budget(default_budget, proposal_tree_budget,
+                                     low_occupancy_tree_budget, low_occupancy_tree_threshold,
+                                     active_count)
+    if (expanded == base or low_occupancy_expansion_slots is None
+            or low_occupancy_expansion_slots >= len(states)):
+        return (expanded,) * len(states)
+    ranked = sorted(states, key=lambda s: (len(s.generated), -s.age, s.request_id))
+    chosen = {s.request_id for s in ranked[:low_occupancy_expansion_slots]}
+    return tuple(expanded if s.request_id in chosen else base for s in states)
+
+
+def adaptive_expansion_eligible(initial_count: int, thresholds: Sequence[int],
+                                requires_drain: bool) -> bool:
+    """Whether the occupancy-dependent expansions may apply to a run of
+    ``initial_count`` requests (CTBD:1303-1314): with ``requires_drain``,
+    only when the run starts above every threshold (a drained tail, not a
+    small run)."""
+    if initial_count < 1 or any(t < 1 for t in thresholds):
+        raise ValueError("Invalid adaptive expansion occupancy")
+    return not requires_drain or not thresholds or initial_count > max(thresholds)
 
 
 def admit_global_proposal_states(states: Sequence, *, row_budget: int,

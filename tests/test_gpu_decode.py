@@ -75,6 +75,29 @@ class _Drafter:
         return S.DraftTree(parents, tokens, depths, masses)
 
 
+class _RolloutDraft:
+    """Per-depth draft probabilities ``q [B, depth, V]`` for DDTree trees: the
+    CPU copy's next-token distributions along its own greedy continuation
+    (a stand-in for the reference's block draft, which emits one
+    distribution per position of the block)."""
+
+    def __init__(self, cpu_model, prompts, depth=4):
+        self.model, self.prompts, self.depth = cpu_model, prompts, depth
+
+    def __call__(self, states):
+        rows = []
+        for s in states:
+            context = list(self.prompts[s.request_id]) + list(s.generated)
+            qs = []
+            for _ in range(self.depth):
+                with torch.no_grad():
+                    logits = self.model(input_ids=torch.tensor(context)[None]).logits[0, -1]
+                qs.append(torch.softmax(logits.float(), -1))
+                context.append(int(qs[-1].argmax()))
+            rows.append(torch.stack(qs))
+        return torch.stack(rows)
+
+
 class _RandomDrafter:
     """The stated workload's drafts: 16-node trees, parents uniform over
     earlier nodes with depth <= 8, draft tokens uniform over the vocabulary."""
@@ -104,26 +127,26 @@ def _prefill(cpu_model, prompts, device):
     return caches, anchors
 
 
-def _decode(setup, device, oracle, *, persistent, drafter, max_new, **kw):
-    from specgrove_amd import decode
-    gpu_model, cpu_model, prompts = setup
-    caches, anchors = _prefill(cpu_model, prompts, device)
-    states = [decode.DecodeRequest(i, [anchors[i]], caches[i],
-                                   torch.Generator(device).manual_seed(77 + i))
-              for i in range(len(prompts))]
-    waves = []
+def _uniforms_from(generator_states, depths, device):
+    """The uniforms each request's generator gave the sampler (two per tree
+    level), redrawn from its state before the draws."""
+    stride = 2 * (max(depths) + 1)
+    uniforms = np.zeros((len(depths), stride), np.float32)
+    for i, (d, gs) in enumerate(zip(depths, generator_states)):
+        g = torch.Generator(device)
+        g.set_state(gs)
+        uniforms[i, :2 * (d + 1)] = torch.rand(2 * (d + 1), dtype=torch.float32,
+                                               device=device, generator=g).cpu().numpy()
+    return uniforms
 
+
+def _wave_checker(oracle, device, waves):
+    """on_wave hook: the oracle sampler on the wave's logits with the uniforms
+    each request's generator gave the verifier must make the same decisions
+    (accepted nodes and tokens, bonus, kept rows)."""
     def check(rec):
-        # The oracle sampler on the wave's logits with the uniforms each
-        # request's generator gave the verifier.
         depths = [max(W.depths_of(list(b.parents))) for b in rec.blocks]
-        stride = 2 * (max(depths) + 1)
-        uniforms = np.zeros((len(rec.blocks), stride), np.float32)
-        for i, (d, gs) in enumerate(zip(depths, rec.generator_states)):
-            g = torch.Generator(device)
-            g.set_state(gs)
-            uniforms[i, :2 * (d + 1)] = torch.rand(2 * (d + 1), dtype=torch.float32,
-                                                   device=device, generator=g).cpu().numpy()
+        uniforms = _uniforms_from(rec.generator_states, depths, device)
         sizes = [len(b.nodes) for b in rec.blocks]
         row_offset = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)
         parent = np.concatenate([np.asarray(b.parents, np.int32) for b in rec.blocks])
@@ -138,6 +161,18 @@ def _decode(setup, device, oracle, *, persistent, drafter, max_new, **kw):
             assert list(rec.keep_rows[i]) == [0] + list(got_nodes)
         waves.append((sizes, [len(r[0]) for r in rec.results]))
         print(f"wave {len(waves)}: rows {sizes} accepted {waves[-1][1]}", flush=True)
+    return check
+
+
+def _decode(setup, device, oracle, *, persistent, drafter, max_new, **kw):
+    from specgrove_amd import decode
+    gpu_model, cpu_model, prompts = setup
+    caches, anchors = _prefill(cpu_model, prompts, device)
+    states = [decode.DecodeRequest(i, [anchors[i]], caches[i],
+                                   torch.Generator(device).manual_seed(77 + i))
+              for i in range(len(prompts))]
+    waves = []
+    check = _wave_checker(oracle, device, waves)
 
     capacity = max(len(p) for p in prompts) + max_new + 64
     result = decode.generate_tree_waves(gpu_model, states, drafter, max_new_tokens=max_new,
@@ -197,12 +232,44 @@ def test_continuation_blocks_and_stop_ids(peaked, device, oracle):
 
 
 def test_global_tiers_respect_the_row_budget(peaked, device, oracle):
-    drafter = _Drafter(peaked[1], peaked[2], width=2, depth=3)
-    res, waves, states = _decode(peaked, device, oracle, persistent=True, drafter=drafter,
-                                 max_new=16, row_cap=64, row_budget=14, global_tiers=(1, 3, 5),
-                                 fixed_row_equivalent=8.0, criticality_weight=1.0)
+    """DDTree trees cut to the allocator's tiers (options 1/3/5 under a 14-row
+    wave budget, the reference's option names and contract)."""
+    from specgrove_amd import ddtree
+    proposer = ddtree.DDTreeProposer(_RolloutDraft(peaked[1], peaked[2]))
+    res, waves, states = _decode(peaked, device, oracle, persistent=True, drafter=proposer,
+                                 max_new=16, row_cap=2, row_budget=14, tree_budget=5,
+                                 global_tree_budget_options=(1, 3, 5),
+                                 continuation_ready_threshold=0,
+                                 global_tree_fixed_row_equivalent=8.0,
+                                 global_tree_criticality_weight=1.0)
     for sizes, _ in waves:
         assert sum(sizes) <= 14 and all(s in (2, 4, 6) for s in sizes)
+    assert {b for b, _ in res.effective_tree_budget_counts} <= {1, 3, 5}
+    assert res.physical_target_rows == res.useful_target_rows == sum(
+        sum(sizes) for sizes, _ in waves)
+
+
+def test_ddtree_trees_with_occupancy_controls(peaked, device, oracle):
+    """DDTree trees from per-depth draft probabilities (the best-first builder
+    of tree.py:148-212), 4-node trees while more than two requests are
+    active and 12-node trees for the one most behind after that, blocks of 5
+    rows widened to 13 at low occupancy; persistent and non-persistent waves
+    agree and every wave matches the oracle."""
+    from specgrove_amd import ddtree
+    proposer = ddtree.DDTreeProposer(_RolloutDraft(peaked[1], peaked[2]))
+    kw = dict(max_new=20, row_cap=5, row_budget=64, tree_budget=12, proposal_tree_budget=4,
+              low_occupancy_tree_budget=12, low_occupancy_tree_threshold=2,
+              low_occupancy_expansion_slots=1, low_occupancy_row_cap=13,
+              low_occupancy_threshold=2)
+    a, waves_a, _ = _decode(peaked, device, oracle, persistent=True, drafter=proposer, **kw)
+    b, waves_b, _ = _decode(peaked, device, oracle, persistent=False, drafter=proposer, **kw)
+    assert a.outputs == b.outputs and waves_a == waves_b
+    budgets = dict(a.effective_tree_budget_counts)
+    caps = dict(a.effective_row_cap_counts)
+    assert set(budgets) <= {4, 12} and budgets[4] >= 4
+    assert set(caps) <= {5, 13} and caps[5] >= 1
+    assert sum(caps.values()) == a.physical_target_calls
+    print("tree budgets", budgets, "row caps", caps, "gated", a.gated_continuations, flush=True)
 
 
 def test_stated_tiny_workload(device, oracle):
@@ -223,28 +290,59 @@ def test_stated_tiny_workload(device, oracle):
 
 
 def test_open_loop_serving(peaked, device, oracle):
-    """Six requests arriving over 40 ms, at most three active: the serving
-    wrapper admits them at wave boundaries, prefills newcomers, runs the
-    non-persistent wave loop and reports per-request latencies."""
+    """Six requests arriving over 40 ms, at most three active, one prompt of
+    300 tokens (two prefill chunks).  Newcomers are prefilled in packed waves
+    through the HIP attention (prompts as causal chains) and their first
+    token drawn by the HIP sampler; the non-persistent wave loop runs between
+    admissions.  Checked: every wave's decisions and every first-token draw
+    against the oracle, the prefilled K/V against the CPU model's prefill,
+    the admission rule at every boundary, and the latency accounting."""
     from specgrove_amd import decode, serving
+    from tests.test_serving import check_admissions
     gpu_model, cpu_model, prompts = peaked
-    prompts = prompts + prompts[:2]
+    rng = np.random.default_rng(21)
+    prompts = prompts + [prompts[0], rng.integers(0, 4096, size=300).tolist()]
     drafter = _Drafter(cpu_model, prompts)
     states = [decode.DecodeRequest(i, [], None, torch.Generator(device).manual_seed(90 + i))
               for i in range(len(prompts))]
+    draws = []
 
-    def prefill(new):
-        caches, anchors = _prefill(cpu_model, [prompts[s.request_id] for s in new], device)
-        for s, c, a in zip(new, caches, anchors):
-            s.target_cache, s.generated = c, [a]
+    def on_chunk(ids, rows, logits, gen_states):
+        uniforms = _uniforms_from(gen_states, [0] * len(ids), device)
+        n = len(ids)
+        _, _, bonus, _, _ = oracle.tree_sample(
+            logits.float().cpu().numpy(), np.arange(n + 1, dtype=np.int32),
+            np.full(n, -1, np.int32), np.full(n, -1, np.int32), uniforms, 0)
+        draws.append((tuple(ids), tuple(int(b) for b in bonus)))
 
+    prefill = serving.PackedPrefill(gpu_model, prompts, on_chunk=on_chunk)
+    waves = []
     arrivals = [0.0, 0.0, 0.005, 0.01, 0.02, 0.04]
     res = serving.serve_open_loop(gpu_model, states, arrivals, drafter, prefill,
-                                  max_active_requests=3, max_new_tokens=10, row_cap=16)
-    assert res.max_concurrent <= 3
+                                  max_active_requests=3, max_new_tokens=10, row_cap=16,
+                                  on_wave=_wave_checker(oracle, device, waves))
+    assert res.max_concurrent <= 3 and len(waves) == res.target_calls
+    check_admissions(res, arrivals, 3)
+    first = {k: s.generated[0] for k, s in enumerate(states)}
+    assert sorted(k for ids, _ in draws for k in ids) == list(range(len(prompts)))
+    for ids, bonus in draws:
+        assert [first[k] for k in ids] == list(bonus)
     for s, m in zip(states, res.request_metrics):
         assert s.done and 1 <= len(s.generated) <= 10 and m["output_tokens"] == len(s.generated)
         assert 0 <= m["queue_ms"] <= m["ttft_ms"] <= m["e2e_ms"]
         assert m["arrival_ms"] <= m["admitted_ms"]
+    # the packed prefill's K/V against the CPU model's own prefill of each prompt
+    probe = [decode.DecodeRequest(k, [], None, torch.Generator(device).manual_seed(5))
+             for k in (0, 5)]
+    serving.PackedPrefill(gpu_model, prompts)(probe)
+    ref, _ = _prefill(cpu_model, [prompts[0], prompts[5]], device)
+    for s, r in zip(probe, ref):
+        assert s.target_cache.get_seq_length() == r.get_seq_length() == len(prompts[s.request_id])
+        for layer, (a, b) in enumerate(zip(s.target_cache.layers, r.layers)):
+            for x, y in ((a.keys, b.keys), (a.values, b.values)):
+                x, y = x.float(), y.float()
+                rel = ((x - y).abs().mean() / y.abs().mean()).item()
+                assert rel <= 1e-2, (s.request_id, layer, rel)
     print("metrics", [(round(m["ttft_ms"], 1), round(m["tpot_ms"], 2))
-                      for m in res.request_metrics], flush=True)
+                      for m in res.request_metrics], "admissions",
+          [a["admitted"] for a in res.admissions], flush=True)

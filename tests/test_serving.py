@@ -70,11 +70,32 @@ def test_admission_respects_arrivals_and_concurrency(monkeypatch):
     assert m[0]["admitted_ms"] == m[1]["admitted_ms"] == 0.0 and m[2]["queue_ms"] > 0
     # request 4 arrives after everything else finished: the loop sleeps until 50 ms
     assert m[4]["admitted_ms"] >= 50.0 and m[4]["queue_ms"] == pytest.approx(0.0, abs=1e-9)
+    check_admissions(res, [0.0, 0.0, 0.0, 0.003, 0.05], 2)
+    assert [a["admitted"] for a in res.admissions] == [(0, 1), (2, 3), (4,)]
     for d in res.request_metrics:
         assert 0 <= d["queue_ms"] <= d["ttft_ms"] <= d["e2e_ms"]
         assert d["service_ms"] == pytest.approx(d["e2e_ms"] - d["queue_ms"])
         assert d["output_tokens"] == 4
         assert d["tpot_ms"] == pytest.approx((d["completed_ms"] - d["first_token_ms"]) / 3)
+
+
+def check_admissions(res, arrivals_s, max_active):
+    """The admission rule of the serving decoder (serving
+    continuous_tree_block_decode.py:1684-1694) on the recorded boundaries:
+    everything that has arrived and is not admitted waits, and the first
+    ``max_active - active`` of those in arrival order are admitted."""
+    admitted_before = set()
+    for entry in res.admissions:
+        waiting = tuple(k for k, a in enumerate(arrivals_s)
+                        if 1000 * a <= entry["at_ms"] and k not in admitted_before)
+        assert entry["waiting"] == waiting
+        assert entry["admitted"] == waiting[:max(0, max_active - entry["active_before"])]
+        admitted_before.update(entry["admitted"])
+    assert admitted_before == set(range(len(arrivals_s)))
+    m = {d["request_id"]: d for d in res.request_metrics}
+    for entry in res.admissions:
+        for k in entry["admitted"]:
+            assert m[k]["admitted_ms"] >= entry["at_ms"]
 
 
 def test_contract_errors():
