@@ -315,7 +315,7 @@ int sg_row_stats(const void* logits_dev, int32_t logits_dtype, int64_t row_strid
  * ---------------------------------------------------------------------- */
 typedef struct SgLmHeadArgs {
   int32_t num_rows;              /* Rp >= 0 rows to project */
-  int32_t hidden_size;           /* H, a positive multiple of 32 */
+  int32_t hidden_size;           /* H, a positive multiple of 64 */
   int32_t vocab;                 /* V >= 1 */
   int32_t num_hidden_rows;       /* rows of hidden_dev (row_index range) */
   const void* hidden_dev;        /* bf16 [num_hidden_rows, hidden_row_stride], < 4 GiB */

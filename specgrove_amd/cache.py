@@ -30,6 +30,40 @@ import torch
 
 from . import ops
 
+_COMMIT_KEEP_STRIDE = 32  # kept rows per request the pool's commit buffers hold at first
+
+
+class DeviceStatus:
+    """A status word that kernels set on a violated contract (SG_EINVAL,
+    SG_ERANGE), read back without a synchronisation of its own.
+
+    ``after_launch()`` enqueues a copy of the word into pinned host memory
+    right behind the kernel; ``check()`` reads that copy once it has landed
+    -- by the next wave the verifier's device-to-host transfer has waited for
+    it -- and raises RuntimeError if a kernel reported an error.  The word is
+    never cleared: an error stays reported.
+    """
+
+    def __init__(self, device, what: str):
+        self.what = what
+        self.dev = torch.zeros(1, dtype=torch.int32, device=device)
+        self.host = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+        self.event = torch.cuda.Event()
+        self.pending = False
+
+    def after_launch(self) -> None:
+        self.host.copy_(self.dev, non_blocking=True)
+        self.event.record()
+        self.pending = True
+
+    def check(self) -> None:
+        if self.pending:
+            self.event.synchronize()
+            self.pending = False
+        code = int(self.host[0])
+        if code != 0:
+            raise RuntimeError(f"{self.what} reported error {code} on the device")
+
 
 def _cache_length(cache) -> int:
     """Cached tokens of a request cache (DynamicCache or arena view)."""
@@ -119,6 +153,14 @@ class PersistentRequestCachePool:
         self.caches = tuple(PersistentRequestCache(self, slot) for slot in range(len(caches)))
         self._k_ptrs = None
         self._v_ptrs = None
+        self._commit = None          # prepared commit call and its metadata buffers
+        self._status = None          # DeviceStatus of the commits, made by the first one
+
+    @property
+    def status(self) -> DeviceStatus:
+        if self._status is None:
+            self._status = DeviceStatus(self.device, "KV commit")
+        return self._status
 
     # -- device mirrors ---------------------------------------------------
     def _device_pointers(self):
@@ -132,6 +174,48 @@ class PersistentRequestCachePool:
         return [cache.slot * self.capacity for cache in caches]
 
     # -- commit -----------------------------------------------------------
+    def _commit_call(self, layers: int, keep_stride: int) -> dict:
+        """The pool's commit call, bound once to persistent metadata buffers
+        sized for every slot (rebuilt only when a wave has more layers or
+        longer keep lists than they hold).  Layout (int64 words): the wave's
+        tree-row pointers per layer (K, then V), the slot starts, then int32
+        pairs: row offsets [slots+1], kept rows [slots, stride], keep lengths
+        [slots], current lengths [slots]."""
+        c = self._commit
+        if c is not None and c["layers"] == layers and c["stride"] >= keep_stride:
+            return c
+        cap = len(self.caches)
+        stride = max(keep_stride, _COMMIT_KEEP_STRIDE, c["stride"] if c else 0)
+        words32 = (cap + 1) + cap * stride + 2 * cap
+        words32 += words32 % 2
+        total = 2 * layers + cap + words32 // 2
+        dev = torch.zeros(total, dtype=torch.int64, device=self.device)
+        host = torch.zeros(total, dtype=torch.int64, pin_memory=True)
+        d32 = dev[2 * layers + cap:].view(torch.int32)
+        base = cap + 1 + cap * stride
+        k_ptrs, v_ptrs = self._device_pointers()
+        k0 = self.key_storage[0]
+        call = ops.prepare_kv_commit(
+            k_ptrs[:layers], v_ptrs[:layers], dev[:layers], dev[layers:2 * layers],
+            num_kv_heads=k0.shape[0], head_dim=k0.shape[2],
+            cache_head_stride=k0.stride(0), cache_token_stride=k0.stride(1),
+            tree_row_stride=k0.shape[2], tree_head_stride=k0.shape[2],
+            row_offset=d32[:cap + 1], keep_rows=d32[cap + 1:base].view(cap, stride),
+            keep_len=d32[base:base + cap], prefix_start=dev[2 * layers:2 * layers + cap],
+            lengths=d32[base + cap:base + 2 * cap], capacity=self.capacity,
+            status=self.status.dev)
+        copied = torch.cuda.Event()
+        copied.record()
+        self._commit = dict(call=call, dev=dev, host=host, layers=layers, slots=cap,
+                            stride=stride, copied=copied)
+        return self._commit
+
+    def check_status(self) -> None:
+        """Raise if a commit kernel reported an error (waits for the last
+        commit's status copy)."""
+        if self._status is not None:
+            self._status.check()
+
     def append_packed_sequence(self, packed: "TreeVerifyCache",
                                caches: Sequence[PersistentRequestCache],
                                packed_old_length: int, query_offsets: Sequence[int],
@@ -144,8 +228,15 @@ class PersistentRequestCachePool:
         row k is ``query_offsets[i] + k`` (the reference's
         ``packed_old_length + query_offsets[i] + k`` in its concatenated
         cache; ``packed_old_length`` must equal the wave's prefix total).
+
+        The call is prepared once per pool; the wave's metadata travels in
+        one host-to-device copy from pinned memory.  The host checks below
+        reject every case the kernel would report; a device-side error of the
+        previous commit still raises here (``status``).
         """
         if not (len(caches) == len(query_offsets) == len(keep_query_rows) and caches):
+            raise ValueError("Persistent cache append metadata disagree")
+        if len({id(c) for c in caches}) != len(caches):
             raise ValueError("Persistent cache append metadata disagree")
         if int(packed_old_length) != packed.prefix_total:
             raise ValueError("Persistent cache append metadata disagree")
@@ -171,41 +262,32 @@ class PersistentRequestCachePool:
                 raise ValueError("Persistent cache append metadata disagree")
             increments.append((cache.slot, increment))
         keep_stride = max(1, max(len(rows) for rows in keep_query_rows))
-        keep = np.full((n, keep_stride), -1, np.int32)
+        commit = self._commit_call(len(packed.layers), keep_stride)
+        self.status.check()
+        # The pinned staging buffer is rewritten only after the previous
+        # wave's copy out of it has completed.
+        commit["copied"].synchronize()
+        slots = [cache.slot for cache in caches]
+        layers, cap, stride = commit["layers"], commit["slots"], commit["stride"]
+        host64 = commit["host"].numpy()
+        host32 = host64[2 * layers + cap:].view(np.int32)
+        host64[:layers] = [layer.tree_keys.data_ptr() for layer in packed.layers]
+        host64[layers:2 * layers] = [layer.tree_values.data_ptr() for layer in packed.layers]
+        host64[2 * layers:2 * layers + n] = [s * self.capacity for s in slots]
+        host32[:n + 1] = row_offset
+        keep = host32[cap + 1:cap + 1 + cap * stride].reshape(cap, stride)
+        keep[:n] = -1
         for i, rows in enumerate(keep_query_rows):
             keep[i, :len(rows)] = [int(r) for r in rows]
-        slots = [cache.slot for cache in caches]
-        k_ptrs, v_ptrs = self._device_pointers()
-        dev = self.device
-        layers = len(packed.layers)
-        # One host-to-device copy: the wave's tree-row pointers per layer, the
-        # requests' slot starts (int64), then row offsets, kept rows, keep
-        # lengths and the current lengths (int32 pairs).  The host lengths are
-        # authoritative; the kernel advances this wave's copy of them.
-        tree_ptrs = [layer.tree_keys.data_ptr() for layer in packed.layers] + \
-                    [layer.tree_values.data_ptr() for layer in packed.layers]
-        words32 = np.concatenate([
-            row_offset.astype(np.int32), keep.reshape(-1),
-            np.asarray([len(r) for r in keep_query_rows], np.int32),
-            np.asarray([self.lengths[s] for s in slots], np.int32)])
-        if words32.size % 2:
-            words32 = np.concatenate([words32, np.zeros(1, np.int32)])
-        host = np.concatenate([np.asarray(tree_ptrs, np.int64),
-                               np.asarray([s * self.capacity for s in slots], np.int64),
-                               words32.view(np.int64)])
-        meta = torch.from_numpy(host).to(dev)
-        meta32 = meta[2 * layers + n:].view(torch.int32)
-        w = keep.size
-        k0 = self.key_storage[0]
+        base = cap + 1 + cap * stride
+        host32[base:base + n] = [len(r) for r in keep_query_rows]
+        host32[base + cap:base + cap + n] = [self.lengths[s] for s in slots]
+        commit["dev"].copy_(commit["host"], non_blocking=True)
+        commit["copied"].record()
         kt = packed.layers[0].tree_keys
-        ops.kv_commit(
-            k_ptrs, v_ptrs, meta[:layers], meta[layers:2 * layers],
-            num_kv_heads=k0.shape[0], head_dim=k0.shape[2],
-            cache_head_stride=k0.stride(0), cache_token_stride=k0.stride(1),
-            tree_row_stride=kt.stride(0), tree_head_stride=kt.stride(1),
-            row_offset=meta32[:n + 1], keep_rows=meta32[n + 1:n + 1 + w].view(n, keep_stride),
-            keep_len=meta32[n + 1 + w:2 * n + 1 + w], prefix_start=meta[2 * layers:2 * layers + n],
-            lengths=meta32[2 * n + 1 + w:3 * n + 1 + w], capacity=self.capacity)
+        commit["call"].set(num_requests=n, tree_row_stride=kt.stride(0),
+                           tree_head_stride=kt.stride(1))()
+        self.status.after_launch()
         for slot, increment in increments:
             self.lengths[slot] += increment
 
@@ -382,7 +464,8 @@ class RequestCache:
 def split_compacted_sequence_caches(packed: TreeVerifyCache, cache_factory,
                                     cache_offsets: Sequence[int], old_lengths: Sequence[int],
                                     packed_old_length: int, query_offsets: Sequence[int],
-                                    keep_query_rows: Sequence[Sequence[int]], device):
+                                    keep_query_rows: Sequence[Sequence[int]], device,
+                                    status: DeviceStatus | None = None):
     """Drop-in for ``_split_compacted_sequence_caches`` (reference :409-450):
     every request's new cache = its old prefix + its kept query rows, for all
     layers in one ``sg_kv_split`` call.
@@ -393,6 +476,10 @@ def split_compacted_sequence_caches(packed: TreeVerifyCache, cache_factory,
     ``cache_factory`` is None).  The source row of request i's kept row k is
     ``query_offsets[i] + k`` of the wave's new rows (the reference's
     ``packed_old_length + query_offsets[i] + k``).
+
+    The checks below reject every kept row or size the kernel would report;
+    with ``status`` (a ``DeviceStatus``, e.g. the wave loop's) a device-side
+    report is also read back and raised by its next ``check()``.
     """
     count = len(cache_offsets)
     if not (count == len(old_lengths) == len(query_offsets) == len(keep_query_rows)
@@ -433,7 +520,6 @@ def split_compacted_sequence_caches(packed: TreeVerifyCache, cache_factory,
         np.asarray(old_lengths, np.int32), row_offset.astype(np.int32),
         np.asarray([len(k) for k in keep_query_rows], np.int32), keep.reshape(-1)])).to(dev)
     kt = packed.layers[0].tree_keys
-    status = torch.zeros(1, dtype=torch.int32, device=dev)
     ops.kv_split(
         ops.pointer_array(source.key_storage[:len(packed.layers)], dev),
         ops.pointer_array(source.value_storage[:len(packed.layers)], dev),
@@ -446,7 +532,10 @@ def split_compacted_sequence_caches(packed: TreeVerifyCache, cache_factory,
         cache_offset=meta[:count], old_length=meta32[:count],
         row_offset=meta32[count:2 * count + 1], keep_len=meta32[2 * count + 1:3 * count + 1],
         keep_rows=meta32[3 * count + 1:].view(count, keep_stride),
-        out_offset=meta[count:], max_tokens=max(sizes), status=status)
+        out_offset=meta[count:], max_tokens=max(sizes),
+        status=status.dev if status is not None else None)
+    if status is not None:
+        status.after_launch()
     results = []
     for i in range(count):
         cache = cache_factory() if cache_factory is not None else RequestCache()

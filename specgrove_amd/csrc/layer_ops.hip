@@ -21,9 +21,11 @@
 //
 // Arithmetic follows the transformers modules' rounding points: RMSNorm
 // normalises in fp32, rounds to bf16, then multiplies by the bf16 weight and
-// rounds again; RoPE uses bf16-rounded cos/sin of fp32 angles; SiLU rounds
+// rounds again; RoPE uses bf16-rounded cos/sin of fp32 angles and rounds
+// q*cos, rotate_half(q)*sin and their sum to bf16 in turn; SiLU rounds
 // before the product with up.  Sums of squares run in fp32 in this kernel's
-// own order.
+// own order, and 1/sqrt and sincos are the device's, so a normed or rotated
+// value can still differ from transformers' by one bf16 ulp.
 #include <cmath>
 
 #include "sg_common.h"
@@ -201,8 +203,12 @@ __global__ __launch_bounds__(kNormThreads) void qk_norm_rope_kernel(
         const float a = bf16_to_f32(t ? (nx[k] >> 16) : (nx[k] & 0xffffu));
         const float b = bf16_to_f32(t ? (ny[k] >> 16) : (ny[k] & 0xffffu));
         const int q = 2 * k + t;
-        // x*cos + rotate_half(x)*sin, rotate_half(x) = (-x2, x1).
-        e[t] = lower ? a * cs[q] - b * sn[q] : a * cs[q] + b * sn[q];
+        // x*cos + rotate_half(x)*sin, rotate_half(x) = (-x2, x1), with the
+        // rounding points of transformers' bf16 tensors: each product is
+        // rounded to bf16, then their sum (bf16r(-v) = -bf16r(v)).
+        const float ac = bf16r(a * cs[q]);
+        const float bs = bf16r(b * sn[q]);
+        e[t] = lower ? ac - bs : ac + bs;
       }
       o[k] = pack_bf16x2(e[0], e[1]);
     }

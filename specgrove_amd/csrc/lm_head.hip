@@ -88,13 +88,13 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // 16-byte HBM -> LDS copy of every lane: lane i's bytes at gbase + voff land
 // at LDS byte lds + 16*i.  Inline assembly, so that the compiler neither
 // models it nor inserts waits for it; the kernel waits explicitly (s_waitcnt
-// vmcnt) before the barrier that publishes a stage.  m0 is written here;
-// nothing else in the kernel reads m0.
+// vmcnt) before the barrier that publishes a stage.  m0 (the LDS base of the
+// copy) is written here and declared clobbered.
 __device__ __forceinline__ void dma16(const void* gbase, uint32_t voff, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                :
                : "s"(lds), "v"(voff), "s"(gbase)
-               : "memory");
+               : "memory", "m0");
 }
 
 // s_waitcnt immediate: vmcnt <= n, the other counters unconstrained.

@@ -170,19 +170,19 @@ __host__ __device__ constexpr int swz_v(int r) {
 // model it: its automatic waits would otherwise stall the first LDS read of the
 // other pipeline stage on this in-flight copy.  The kernel waits for the DMAs
 // explicitly (s_waitcnt vmcnt(0)) before the barrier that publishes the tile.
-// m0 is written here; nothing else in the kernel reads m0.
+// m0 (the LDS base of the copy) is written here and declared clobbered.
 template <bool kStream>
 __device__ __forceinline__ void dma16(const void* gbase, uint32_t voff, uint32_t lds) {
   if constexpr (kStream) {
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt"
                  :
                  : "s"(lds), "v"(voff), "s"(gbase)
-                 : "memory");
+                 : "memory", "m0");
   } else {
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                  :
                  : "s"(lds), "v"(voff), "s"(gbase)
-                 : "memory");
+                 : "memory", "m0");
   }
 }
 // Run-time choice for the unit's rare issue paths (prologue, partial and tree tiles).

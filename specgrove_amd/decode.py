@@ -286,6 +286,8 @@ class WaveLoop:
         self.device = next(model.parameters()).device
         self.dtype = next(model.parameters()).dtype
         self.pool = None
+        self.split_status = (cache_mod.DeviceStatus(self.device, "KV split")
+                             if not persistent and self.device.type == "cuda" else None)
         self.expansion_eligible = True
         self.stage = {"prefill": 0.0, "proposal": 0.0, "target": 0.0, "pack": 0.0,
                       "select_commit": 0.0}
@@ -440,8 +442,11 @@ class WaveLoop:
         if self.pool is not None:
             self.pool.append_packed_sequence(packed, caches, total, qoff, keeps, self.device)
         else:
+            if self.split_status is not None:
+                self.split_status.check()
             new = cache_mod.split_compacted_sequence_caches(
-                packed, self.cache_factory, offsets, lengths, total, qoff, keeps, self.device)
+                packed, self.cache_factory, offsets, lengths, total, qoff, keeps, self.device,
+                status=self.split_status)
             for s, c in zip(chosen, new):
                 s.target_cache = c
         if self.on_wave is not None:
@@ -493,6 +498,13 @@ class WaveLoop:
             s.done = True
             return True
         return False
+
+    def check_status(self) -> None:
+        """Raise if a commit or split kernel of this loop reported an error."""
+        if self.pool is not None:
+            self.pool.check_status()
+        if self.split_status is not None:
+            self.split_status.check()
 
     def result(self, states: Sequence[DecodeRequest], wall_s: float) -> "DecodeResult":
         """The run's outputs and accounting (CTBD:2252-2270)."""
@@ -546,4 +558,5 @@ def generate_tree_waves(model, states: Sequence[DecodeRequest], propose, *,
             raise RuntimeError("Decode did not finish within max_waves")
         loop.step(states)
     torch.cuda.synchronize(loop.device)
+    loop.check_status()
     return loop.result(states, time.perf_counter() - wall0)

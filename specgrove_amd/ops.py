@@ -52,6 +52,16 @@ class PreparedCall:
         _lib.check(self._fn(self._ref, _stream_handle()), self._name)
         return self.result
 
+    def set(self, **fields) -> "PreparedCall":
+        """Update scalar fields of the bound argument struct (sizes and
+        strides that change from call to call over the same buffers, e.g. a
+        commit's request count); the library checks them on every call."""
+        for name, value in fields.items():
+            if not hasattr(self._args, name):
+                raise ValueError(f"{self._name} has no argument {name}")
+            setattr(self._args, name, value)
+        return self
+
 
 def _require(cond: bool, message: str) -> None:
     if not cond:

@@ -221,6 +221,7 @@ def serve_open_loop(model, states: Sequence[DecodeRequest],
             for s in finished:
                 done_at[index[id(s)]] = t
     wall = clock() - start
+    loop.check_status()
     if any(v is None for v in admitted_at + first_at + done_at):
         raise RuntimeError("Open-loop request timing is incomplete")
     metrics = []

@@ -32,6 +32,9 @@ def _fake_loop(clock, log):
             for s in states:
                 s.done = len(s.generated) >= 99
 
+        def check_status(self):
+            pass
+
         def step(self, states):
             log.append(tuple(s.request_id for s in states))
             clock.t += 0.002
