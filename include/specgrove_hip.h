@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define SG_ABI_VERSION 4
+#define SG_ABI_VERSION 5
 
 #define SG_OK 0
 #define SG_EINVAL (-1)  /* shape or contract violation (Python: ValueError) */
@@ -247,9 +247,12 @@ typedef struct SgTreeSampleArgs {
   int32_t* keep_rows_dev;        /* optional [n, max_depth+1]: [0] + nodes, -1 padded */
   int32_t* status_dev;           /* optional [1]: cleared to 0 by the call, then
                                     SG_EINVAL if a walk broke the contract */
-  void* workspace_dev;           /* >= sg_tree_sample_workspace_bytes(): per-slab
-                                    and per-line complement totals of the exit rows,
-                                    and each request's exit node and its children */
+  void* workspace_dev;           /* >= sg_tree_sample_workspace_bytes(): each
+                                    statistics row's slab pairs (max and sum of
+                                    exp per 2048-token slab), and for the
+                                    complement draw per-slab and per-line totals
+                                    of the exit rows and each request's exit node
+                                    and children */
   size_t workspace_bytes;
   /* Lazy projection (FTS:2840-3019, SMP:738-832): only the rows a walk can
    * route from were projected (sg_lm_head below). */
@@ -273,13 +276,16 @@ typedef struct SgTreeSampleArgs {
 /* Row statistics of all packed rows followed by the per-request walk. */
 int sg_tree_sample(const SgTreeSampleArgs* args, sg_stream_t stream);
 
-/* Scratch bytes sg_tree_sample needs for num_requests requests over vocab
- * (36 bytes per 2048-token slab per request, plus 4,112 bytes per request).
- * No reference counterpart. */
-int64_t sg_tree_sample_workspace_bytes(int32_t num_requests, int32_t vocab);
+/* Scratch bytes sg_tree_sample needs for num_requests requests over vocab,
+ * with num_rows statistics rows: the rows whose statistics the call computes
+ * (num_logits_rows, or num_rows without a row map), 0 with
+ * SG_SAMPLE_STATS_READY.  Per 2048-token slab 8 bytes per statistics row and
+ * 36 bytes per request, plus 4,112 bytes per request.  No reference
+ * counterpart. */
+int64_t sg_tree_sample_workspace_bytes(int32_t num_requests, int32_t num_rows, int32_t vocab);
 
 /* Size of the static per-GPU scratch of sg_tree_sample_noalloc (4 MiB: e.g.
- * 615 requests at vocab 151,936). */
+ * 128 requests and 4,096 statistics rows at vocab 151,936). */
 #define SG_TREE_SAMPLE_NOALLOC_SCRATCH_BYTES (4u << 20)
 
 /* sg_tree_sample without any device allocation: the workspace is a static

@@ -76,6 +76,14 @@ def lib() -> ctypes.CDLL:
             i32p, f32p, ctypes.c_int32, ctypes.c_int32, i32p, f32p, f32p,
             i32p, i32p, i32p, i32p,
         ]
+        handle.sgo_rows_slab_stats.restype = None
+        handle.sgo_rows_slab_stats.argtypes = [f32p, ctypes.c_int64, ctypes.c_int64,
+                                               ctypes.c_int32, f32p, f32p, f32p]
+        handle.sgo_slab_draw.restype = ctypes.c_int32
+        handle.sgo_slab_draw.argtypes = [
+            f32p, ctypes.c_int64, ctypes.c_float, f32p, i32p, ctypes.c_int,
+            ctypes.c_float, f32p,
+        ]
         handle.sgo_lm_head_tile_stats.restype = None
         handle.sgo_lm_head_tile_stats.argtypes = [f32p, ctypes.c_int64, f32p]
         handle.sgo_lm_head_row_stats.restype = None
@@ -111,6 +119,33 @@ def row_stats(row: np.ndarray) -> tuple[float, float]:
     return float(m[0]), float(z[0])
 
 
+def slab_stats(logits: np.ndarray) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Row statistics of the sampler's own statistics pass (sg_oracle.c,
+    sgo_row_slab_stats): per row (max, sum of exp) and, per 2048-token slab,
+    (m_s, Z_s) -- the slab max and its sum of E(x - m_s)."""
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    rows, vocab = logits.shape
+    slabs = (vocab + 2047) // 2048
+    m = np.zeros(rows, np.float32)
+    z = np.zeros(rows, np.float32)
+    ss = np.zeros((rows, slabs, 2), np.float32)
+    lib().sgo_rows_slab_stats(_f32p(logits), vocab, vocab, rows, _f32p(m), _f32p(z), _f32p(ss))
+    return m, z, ss
+
+
+def slab_draw(row: np.ndarray, m: float, row_slab_stats: np.ndarray,
+              child_tokens: Sequence[int], u: float) -> tuple[int, float]:
+    """The exit draw from one row's slab statistics (sgo_slab_draw): the
+    bonus token and the complement total C."""
+    row = np.ascontiguousarray(row, dtype=np.float32)
+    ss = np.ascontiguousarray(row_slab_stats, dtype=np.float32)
+    children = np.ascontiguousarray(np.asarray(child_tokens, np.int32))
+    total = np.zeros(1, np.float32)
+    token = lib().sgo_slab_draw(_f32p(row), row.size, np.float32(m), _f32p(ss),
+                                _i32p(children), children.size, np.float32(u), _f32p(total))
+    return int(token), float(total[0])
+
+
 def complement_draw(row: np.ndarray, m: float, child_tokens: Sequence[int],
                     u: float) -> tuple[int, float]:
     row = np.ascontiguousarray(row, dtype=np.float32)
@@ -130,8 +165,10 @@ def tree_sample(logits: np.ndarray, row_offset: np.ndarray, parent: np.ndarray,
 
     ``logits`` [rows, V] fp32, ``row_offset`` [n+1], ``parent``/``token``
     [rows] int32 (request-local parent, -1 root), ``uniforms`` [n, U] fp32.
-    Returns (accept_nodes [n, max_depth], accept_len [n], bonus [n],
-    row_m [rows], row_z [rows]).  Requests are independent, so ``threads`` > 1
+    Statistics are computed here, as the sampler's own pass computes them,
+    and the exit draw is the slab draw (sgo_slab_draw).  Returns
+    (accept_nodes [n, max_depth], accept_len [n], bonus [n], row_m [rows],
+    row_z [rows]).  Requests are independent, so ``threads`` > 1
     runs contiguous groups of requests in parallel C calls (same results).
     """
     logits = np.ascontiguousarray(logits, dtype=np.float32)
@@ -216,7 +253,8 @@ def tree_sample_mapped(logits: np.ndarray, row_offset: np.ndarray, parent: np.nd
     ``logits`` [logits rows, V] fp32; ``row_map`` [rows] gives each packed
     node's logits row (-1: not projected, only for nodes without children;
     None: row r); ``row_m``/``row_z`` [logits rows] are given statistics (the
-    LM head's) or None (computed as the sampler's own pass does).  Returns
+    LM head's; the exit is then the complement draw, sgo_complement_draw) or
+    None (computed as the sampler's own pass does, with the slab draw).  Returns
     (accept_nodes [n, max_depth], accept_len [n], bonus [n], terminal_leaf [n]);
     bonus is -1 where the walk ended at an unprojected leaf.
     """

@@ -33,14 +33,27 @@
  *          (slab s, line j in [0,8), lane l in [0,64), component c in [0,4)).
  *   row stats (m, Z):
  *          per slab: m_s = max; lane partial a_c = sum over j (ascending) of
- *          E(x - m_s); lane sum (a0+a1)+(a2+a3); slab sum by an xor butterfly
- *          over the 64 lanes (distances 32,16,8,4,2,1).  Slab (m_s, Z_s) pairs
- *          are merged into lane (s mod 64) in ascending s, then the 64 lane
- *          pairs are merged by the same xor butterfly; merge(a,b) =
- *          (M, a.z*E(a.m-M) + b.z*E(b.m-M)), M = max(a.m, b.m).
+ *          E(x - m_s); lane sum (a0+a1)+(a2+a3); slab sum Z_s by an xor
+ *          butterfly over the 64 lanes (distances 32,16,8,4,2,1).  Slab
+ *          (m_s, Z_s) pairs are merged into lane (s mod 64) in ascending s,
+ *          then the 64 lane pairs are merged by the same xor butterfly;
+ *          merge(a,b) = (M, a.z*E(a.m-M) + b.z*E(b.m-M)), M = max(a.m, b.m).
+ *          The slab pairs of every row are kept.
  *   routing at node v: children in ascending node order; S += E(x[tok]-m_v);
  *          accept the first child with u[2d]*Z_v < S.
- *   exit at node v: e_t = 0 for child tokens, else E(x_t - m_v);
+ *   exit at node v when the sampler computed the statistics (slab draw):
+ *          Z'_s = Z_s, or for a slab holding a child token the same sums with
+ *          the child terms 0; E_s = E(m_s - M) (M = m_v), w_s = Z'_s * E_s;
+ *          P_0 = 0, P_(s+1) = P_s + w_s, C = P_S; threshold u[2d+1]*C; the
+ *          slab is the first s with P_s + w_s > threshold; in it, per line,
+ *          e_t = E(x_t - m_s) (0 for child tokens), group sums, an inclusive
+ *          Kogge-Stone scan over the 64 lanes and sequential line prefixes
+ *          Q_j; for token c of lane l in line j, r = (Q_j + EX_jl) + e_0 +
+ *          ... + e_c; the bonus is the first non-child token with
+ *          P_s + E_s*r > threshold, else the slab's last non-child token with
+ *          e_t > 0; no slab crossing: the largest non-child token.
+ *   exit at node v with given statistics (the LM head's; complement draw):
+ *          e_t = 0 for child tokens, else E(x_t - m_v);
  *          group sum ((e0+e1)+e2)+e3 per (s,j,l); inclusive Kogge-Stone scan
  *          over the 64 lanes of a line (distances 1..32); line prefix and slab
  *          prefix sequential; complement total C = last slab prefix;
@@ -131,7 +144,23 @@ static float sgo_butterfly_sum(float* v) {
   return v[0];
 }
 
+/* (m_s, Z_s) of slab s; with skip (child tokens, count) those tokens' terms
+ * are 0 (the complement of one slab, same order). */
+static sgo_mz sgo_slab_stats_skip(const float* x, int64_t vocab, int64_t slab,
+                                  const int32_t* skip, int skip_count);
+
 static sgo_mz sgo_slab_stats(const float* x, int64_t vocab, int64_t slab) {
+  return sgo_slab_stats_skip(x, vocab, slab, 0, 0);
+}
+
+static int sgo_is_child_token(int64_t t, const int32_t* child_tokens, int child_count) {
+  for (int k = 0; k < child_count; ++k)
+    if (child_tokens[k] == t) return 1;
+  return 0;
+}
+
+static sgo_mz sgo_slab_stats_skip(const float* x, int64_t vocab, int64_t slab,
+                                  const int32_t* skip, int skip_count) {
   const int64_t base = slab * SGO_SLAB;
   float m = -INFINITY;
   for (int64_t t = base; t < base + SGO_SLAB && t < vocab; ++t) m = fmaxf(m, x[t]);
@@ -147,7 +176,8 @@ static sgo_mz sgo_slab_stats(const float* x, int64_t vocab, int64_t slab) {
     for (int j = 0; j < SGO_LINES_PER_SLAB; ++j) {
       for (int c = 0; c < 4; ++c) {
         int64_t t = base + (int64_t)SGO_LINE * j + 4 * l + c;
-        if (t < vocab) a[c] = a[c] + sgo_exp(x[t] - m);
+        if (t < vocab && !sgo_is_child_token(t, skip, skip_count))
+          a[c] = a[c] + sgo_exp(x[t] - m);
       }
     }
     lane[l] = (a[0] + a[1]) + (a[2] + a[3]);
@@ -157,8 +187,10 @@ static sgo_mz sgo_slab_stats(const float* x, int64_t vocab, int64_t slab) {
   return out;
 }
 
-/* Canonical (max, sum of exp) of one logits row. */
-void sgo_row_stats(const float* x, int64_t vocab, float* out_m, float* out_z) {
+/* Canonical (max, sum of exp) of one logits row; slab_stats (when not NULL,
+ * [slabs][2]) receives each slab's (m_s, Z_s). */
+void sgo_row_slab_stats(const float* x, int64_t vocab, float* out_m, float* out_z,
+                        float* slab_stats) {
   sgo_mz lane[SGO_LANES];
   for (int l = 0; l < SGO_LANES; ++l) {
     lane[l].m = -INFINITY;
@@ -167,7 +199,12 @@ void sgo_row_stats(const float* x, int64_t vocab, float* out_m, float* out_z) {
   const int64_t slabs = (vocab + SGO_SLAB - 1) / SGO_SLAB;
   for (int64_t s = 0; s < slabs; ++s) {
     int l = (int)(s % SGO_LANES);
-    lane[l] = sgo_merge(lane[l], sgo_slab_stats(x, vocab, s));
+    const sgo_mz slab = sgo_slab_stats(x, vocab, s);
+    if (slab_stats) {
+      slab_stats[2 * s] = slab.m;
+      slab_stats[2 * s + 1] = slab.z;
+    }
+    lane[l] = sgo_merge(lane[l], slab);
   }
   sgo_mz t[SGO_LANES];
   for (int d = 32; d >= 1; d >>= 1) {
@@ -178,11 +215,10 @@ void sgo_row_stats(const float* x, int64_t vocab, float* out_m, float* out_z) {
   *out_z = lane[0].z;
 }
 
-static int sgo_is_child_token(int64_t t, const int32_t* child_tokens, int child_count) {
-  for (int k = 0; k < child_count; ++k)
-    if (child_tokens[k] == t) return 1;
-  return 0;
+void sgo_row_stats(const float* x, int64_t vocab, float* out_m, float* out_z) {
+  sgo_row_slab_stats(x, vocab, out_m, out_z, 0);
 }
+
 
 /* Complement draw of one row: returns the bonus token and stores C. */
 int32_t sgo_complement_draw(const float* x, int64_t vocab, float m,
@@ -260,6 +296,73 @@ int32_t sgo_complement_draw(const float* x, int64_t vocab, float m,
   return -1;
 }
 
+/* Slab draw of the exit row from its statistics-pass slab pairs (m_s, Z_s):
+ * returns the bonus token and stores C. */
+int32_t sgo_slab_draw(const float* x, int64_t vocab, float m_row, const float* slab_stats,
+                      const int32_t* child_tokens, int child_count, float u,
+                      float* out_total) {
+  const int64_t slabs = (vocab + SGO_SLAB - 1) / SGO_SLAB;
+  float* es = (float*)__builtin_alloca(sizeof(float) * (size_t)slabs);
+  float* w = (float*)__builtin_alloca(sizeof(float) * (size_t)slabs);
+  for (int64_t s = 0; s < slabs; ++s) {
+    float zs = slab_stats[2 * s + 1];
+    int has_child = 0;
+    for (int k = 0; k < child_count; ++k)
+      has_child |= child_tokens[k] >= s * SGO_SLAB && child_tokens[k] < (s + 1) * SGO_SLAB;
+    if (has_child) zs = sgo_slab_stats_skip(x, vocab, s, child_tokens, child_count).z;
+    es[s] = sgo_exp(slab_stats[2 * s] - m_row);
+    w[s] = zs * es[s];
+  }
+  float total = 0.0f;
+  for (int64_t s = 0; s < slabs; ++s) total = total + w[s];
+  if (out_total) *out_total = total;
+  const float threshold = u * total;
+  float p = 0.0f;
+  for (int64_t s = 0; s < slabs; ++s) {
+    if (!(p + w[s] > threshold)) {
+      p = p + w[s];
+      continue;
+    }
+    /* The crossing slab: per line group sums, an inclusive Kogge-Stone scan
+     * over the 64 lanes and sequential line prefixes; running values scaled
+     * by E(m_s - M). */
+    const float ms = slab_stats[2 * s];
+    int32_t last = -1;
+    float q = 0.0f;
+    for (int j = 0; j < SGO_LINES_PER_SLAB; ++j) {
+      float e[SGO_LANES][4], incl[SGO_LANES], tmp[SGO_LANES];
+      const int64_t t0 = s * SGO_SLAB + (int64_t)SGO_LINE * j;
+      for (int l = 0; l < SGO_LANES; ++l) {
+        for (int c = 0; c < 4; ++c) {
+          const int64_t t = t0 + 4 * l + c;
+          e[l][c] = (t < vocab && !sgo_is_child_token(t, child_tokens, child_count))
+                        ? sgo_exp(x[t] - ms) : 0.0f;
+        }
+        incl[l] = ((e[l][0] + e[l][1]) + e[l][2]) + e[l][3];
+      }
+      for (int d = 1; d < SGO_LANES; d <<= 1) {
+        for (int l = 0; l < SGO_LANES; ++l) tmp[l] = (l >= d) ? incl[l] + incl[l - d] : incl[l];
+        memcpy(incl, tmp, sizeof(tmp));
+      }
+      for (int l = 0; l < SGO_LANES; ++l) {
+        float r = q + (l ? incl[l - 1] : 0.0f);
+        for (int c = 0; c < 4; ++c) {
+          const int64_t t = t0 + 4 * l + c;
+          r = r + e[l][c];
+          if (t >= vocab || sgo_is_child_token(t, child_tokens, child_count)) continue;
+          if (p + es[s] * r > threshold) return (int32_t)t;
+          if (e[l][c] > 0.0f) last = (int32_t)t;
+        }
+      }
+      q = q + incl[SGO_LANES - 1];
+    }
+    return last;
+  }
+  for (int64_t t = vocab - 1; t >= 0; --t)
+    if (!sgo_is_child_token(t, child_tokens, child_count)) return (int32_t)t;
+  return -1;
+}
+
 /*
  * Sample every request of a packed wave.
  *   logits      [logits rows, row_stride] fp32 (only the first vocab entries used)
@@ -271,7 +374,8 @@ int32_t sgo_complement_draw(const float* x, int64_t vocab, float m,
  *   row_map     optional [rows]: logits row of each packed node, -1 when the node
  *               was not projected (then it must have no children); NULL: row r
  *   row_m_in, row_z_in  optional [logits rows]: given row statistics (the LM
- *               head's); NULL: computed by sgo_row_stats
+ *               head's), with the complement draw at the exit; NULL: computed by
+ *               sgo_row_slab_stats, with the slab draw at the exit
  * Outputs: accept_nodes [n, max_depth] (local node ids, -1 padded),
  *          accept_len [n], bonus [n] (-1 at an unprojected terminal leaf),
  *          terminal_leaf [n] (may be NULL: that leaf's local id, else -1).
@@ -286,6 +390,8 @@ int sgo_tree_sample_mapped(const float* logits, int64_t row_stride, int64_t voca
                            int32_t* accept_nodes, int32_t* accept_len, int32_t* bonus,
                            int32_t* terminal_leaf) {
   if (num_requests < 0 || vocab < 1 || max_depth < 0) return SGO_EINVAL;
+  const int64_t slabs = (vocab + SGO_SLAB - 1) / SGO_SLAB;
+  float* slab_stats = (float*)__builtin_alloca(sizeof(float) * (size_t)(2 * slabs));
   for (int32_t i = 0; i < num_requests; ++i) {
     const int32_t r0 = row_offset[i];
     const int32_t n = row_offset[i + 1] - r0;
@@ -317,11 +423,12 @@ int sgo_tree_sample_mapped(const float* logits, int64_t row_stride, int64_t voca
       }
       const float* x = logits + (int64_t)lrow * row_stride;
       float m, z;
-      if (row_m_in && row_z_in) {
+      const int given = row_m_in && row_z_in;
+      if (given) {
         m = row_m_in[lrow];
         z = row_z_in[lrow];
       } else {
-        sgo_row_stats(x, vocab, &m, &z);
+        sgo_row_slab_stats(x, vocab, &m, &z, slab_stats);
       }
       const float route_threshold = u[2 * depth] * z;
       float cumulative = 0.0f;
@@ -341,7 +448,10 @@ int sgo_tree_sample_mapped(const float* logits, int64_t row_stride, int64_t voca
         continue;
       }
       accept_len[i] = depth;
-      bonus[i] = sgo_complement_draw(x, vocab, m, child_tokens, count, u[2 * depth + 1], 0);
+      bonus[i] = given ? sgo_complement_draw(x, vocab, m, child_tokens, count,
+                                             u[2 * depth + 1], 0)
+                       : sgo_slab_draw(x, vocab, m, slab_stats, child_tokens, count,
+                                       u[2 * depth + 1], 0);
       break;
     }
   }
@@ -349,7 +459,7 @@ int sgo_tree_sample_mapped(const float* logits, int64_t row_stride, int64_t voca
 }
 
 /* The unmapped sampler: every packed row has logits, statistics computed here
- * (row_m / row_z, when given, receive them). */
+ * (row_m / row_z, when given, receive them) and the slab draw at the exit. */
 int sgo_tree_sample(const float* logits, int64_t row_stride, int64_t vocab,
                     int32_t num_requests, const int32_t* row_offset,
                     const int32_t* parent, const int32_t* token,
@@ -364,8 +474,7 @@ int sgo_tree_sample(const float* logits, int64_t row_stride, int64_t vocab,
       sgo_row_stats(logits + (int64_t)r * row_stride, vocab, &row_m[r], &row_z[r]);
   }
   return sgo_tree_sample_mapped(logits, row_stride, vocab, num_requests, row_offset, parent,
-                                token, uniforms, uniform_stride, max_depth, 0,
-                                (row_m && row_z) ? row_m : 0, (row_m && row_z) ? row_z : 0,
+                                token, uniforms, uniform_stride, max_depth, 0, 0, 0,
                                 accept_nodes, accept_len, bonus, 0);
 }
 
@@ -418,6 +527,15 @@ void sgo_lm_head_row_stats(const float* pairs, int64_t tiles, float* out_m, floa
   }
   *out_m = lane[0].m;
   *out_z = lane[0].z;
+}
+
+/* Slab statistics of many rows ([rows][slabs][2]), for tests of the GPU's. */
+void sgo_rows_slab_stats(const float* logits, int64_t row_stride, int64_t vocab, int32_t rows,
+                         float* row_m, float* row_z, float* slab_stats) {
+  const int64_t slabs = (vocab + SGO_SLAB - 1) / SGO_SLAB;
+  for (int32_t r = 0; r < rows; ++r)
+    sgo_row_slab_stats(logits + (int64_t)r * row_stride, vocab, &row_m[r], &row_z[r],
+                       slab_stats + (int64_t)r * 2 * slabs);
 }
 
 /* Vectorised E(x) for tests of the exp restatement. */

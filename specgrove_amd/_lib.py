@@ -16,7 +16,7 @@ SG_EINVAL = -1
 SG_ERANGE = -2
 SG_EHIP = -3
 
-SG_ABI_VERSION = 4
+SG_ABI_VERSION = 5
 SG_DTYPE_F32 = 0
 SG_DTYPE_BF16 = 1
 SG_DTYPE_F16 = 2
@@ -186,7 +186,7 @@ def load() -> ctypes.CDLL:
     lib.sg_tree_sample_noalloc.restype = c_i32
     lib.sg_tree_sample_noalloc.argtypes = [ctypes.POINTER(SgTreeSampleArgs), c_void_p]
     lib.sg_tree_sample_workspace_bytes.restype = c_i64
-    lib.sg_tree_sample_workspace_bytes.argtypes = [c_i32, c_i32]
+    lib.sg_tree_sample_workspace_bytes.argtypes = [c_i32, c_i32, c_i32]
     lib.sg_row_stats.restype = c_i32
     lib.sg_row_stats.argtypes = [c_void_p, c_i32, c_i64, c_i32, c_i32, c_void_p, c_void_p,
                                  c_void_p]

@@ -20,9 +20,20 @@
 //     lane s%64; final xor butterfly merge over the 64 lanes.
 //   routing:  S += E(x[child token] - m) over children in node order; accept
 //     the first child with u*Z < S.
-//   exit: group sums ((e0+e1)+e2)+e3, inclusive Kogge-Stone scan over the 64
-//     lanes of a line, sequential line and slab prefixes; the bonus is the
-//     first non-child token whose running value exceeds u*C.
+//   exit, slab draw (statistics computed by this call, which keeps every
+//     row's slab pairs (m_s, Z_s)): Z'_s = Z_s, or for a slab holding a child
+//     token the same sums with the child terms left out; w_s = Z'_s *
+//     E(m_s - M); sequential prefixes P_s, C = P_S; the first slab with
+//     P_s + w_s > u*C; in it group sums of e = E(x - m_s), an inclusive
+//     Kogge-Stone scan over the 64 lanes of each line and sequential line
+//     prefixes; the bonus is the first non-child token whose running value
+//     P_s + E(m_s - M) * r exceeds u*C, else the slab's last non-child token
+//     with e > 0.
+//   exit, complement draw (statistics given, SG_SAMPLE_STATS_READY): group
+//     sums ((e0+e1)+e2)+e3 of e = E(x - M), inclusive Kogge-Stone scan over
+//     the 64 lanes of a line, sequential line and slab prefixes; the bonus is
+//     the first non-child token whose running value exceeds u*C.
+//   Either way the fallback is the largest non-child token.
 #pragma clang fp contract(off)
 
 #include <limits.h>
@@ -49,6 +60,8 @@ constexpr int kMaxTreeRows = 1024;
 // walk), exit node, child count, exit logits row (-1: an unprojected leaf), then
 // the exit node's child tokens.
 constexpr int kRecordInts = 4 + kMaxTreeRows;
+// Slab statistics of a statistics row: per slab (m_s, Z_s).
+constexpr int kSlabStats = 2;
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -222,10 +235,13 @@ __device__ __forceinline__ MZ slab_stats(const float v[32]) {
 // number of (row, slab) tasks.
 // Workgroup 0 also clears the caller's status word (when given): the later
 // kernels of the call only ever raise it.
+// With slab_out the row's slab pairs (m_s, Z_s) are also written there, once
+// the slabs are done (600 bytes a row at vocab 151,936).
 template <typename S, bool kVec>
 __global__ __launch_bounds__(kStatsThreads, 2) void row_stats_kernel(
     const S* __restrict__ logits, int64_t row_stride, int vocab, int rows,
-    float* __restrict__ row_max, float* __restrict__ row_sum, int32_t* __restrict__ status) {
+    float* __restrict__ row_max, float* __restrict__ row_sum, float* __restrict__ slab_out,
+    int32_t* __restrict__ status) {
   __shared__ float s_m[kMaxSlabs];
   __shared__ float s_z[kMaxSlabs];
   const int lane = threadIdx.x & (kWave - 1);
@@ -286,6 +302,11 @@ __global__ __launch_bounds__(kStatsThreads, 2) void row_stats_kernel(
     s = next2;
   }
   __syncthreads();
+  if (slab_out != nullptr) {
+    float2* __restrict__ out =
+        reinterpret_cast<float2*>(slab_out) + static_cast<int64_t>(row) * slabs;
+    for (int k = threadIdx.x; k < slabs; k += kStatsThreads) out[k] = make_float2(s_m[k], s_z[k]);
+  }
   if (wave != 0) return;
   MZ acc = {-__builtin_inff(), 0.0f};
   for (int t = lane; t < slabs; t += kWave) {
@@ -732,6 +753,192 @@ __global__ __launch_bounds__(kWave) void exit_find_kernel(SgTreeSampleArgs a) {
   }
 }
 
+// Sum of E(x - m) over one slab in the statistics pass's order (lane
+// partials over the lines, (a0+a1)+(a2+a3), butterfly), leaving out the
+// child tokens of `bits` (bit 4j+c: token 2048s + 256j + 4*lane + c).
+__device__ __forceinline__ float slab_sum_skip(const float v[32], float m, uint32_t bits) {
+  float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+  if (m != -__builtin_inff()) {
+#pragma unroll
+    for (int j = 0; j < kLinesPerSlab; ++j) {
+      const float e0 = sg_exp_nonpos(v[4 * j + 0] - m);
+      const float e1 = sg_exp_nonpos(v[4 * j + 1] - m);
+      const float e2 = sg_exp_nonpos(v[4 * j + 2] - m);
+      const float e3 = sg_exp_nonpos(v[4 * j + 3] - m);
+      a0 = ((bits >> (4 * j + 0)) & 1u) ? a0 : a0 + e0;
+      a1 = ((bits >> (4 * j + 1)) & 1u) ? a1 : a1 + e1;
+      a2 = ((bits >> (4 * j + 2)) & 1u) ? a2 : a2 + e2;
+      a3 = ((bits >> (4 * j + 3)) & 1u) ? a3 : a3 + e3;
+    }
+  }
+  return wave_butterfly_sum((a0 + a1) + (a2 + a3));
+}
+
+// The walk with the slab draw, when the statistics pass of this call kept
+// every row's slab pairs (no SG_SAMPLE_STATS_READY).  One workgroup per
+// request: route (route_request), then from the exit row's slab pairs:
+//   1. the slabs that hold a child token of the exit node are summed again
+//      without those tokens (one wave per slab, the pass's order);
+//   2. per slab w_s = Z'_s * E(m_s - M), then the sequential prefixes P_s
+//      and C;
+//   3. the first slab with P_s + w_s > u*C, and in it the first non-child
+//      token whose running value (per line group sums, inclusive Kogge-Stone
+//      scan over the 64 lanes, sequential line prefixes) exceeds u*C -- else
+//      the slab's last non-child token with e > 0; no slab: the largest
+//      non-child token.
+// Four dependent memory round trips: the tree, the statistics and child
+// logits, the exit row's slab pairs and child slabs, the crossing slab.
+template <typename S, bool kVec>
+__global__ __launch_bounds__(kWalkThreads) void slab_walk_kernel(
+    SgTreeSampleArgs a, const float* __restrict__ slab_stats) {
+  __shared__ RouteShared sh;
+  __shared__ float s_m[kMaxSlabs];
+  __shared__ float s_z[kMaxSlabs];   // Z_s, then Z'_s in place
+  __shared__ float s_w[kMaxSlabs];
+  __shared__ float s_es[kMaxSlabs];
+  __shared__ float s_p[kMaxSlabs];
+  __shared__ unsigned char s_child_slab[kMaxSlabs];
+  __shared__ float s_thr;
+  const int req = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int r0 = a.row_offset_dev[req];
+  const int n = a.row_offset_dev[req + 1] - r0;
+  if (n < 1 || n > kMaxTreeRows || r0 < 0 || r0 > a.num_rows - n) {
+    if (tid == 0) {
+      a.accept_len_dev[req] = -1;
+      a.bonus_dev[req] = -1;
+      if (a.terminal_leaf_dev) a.terminal_leaf_dev[req] = -1;
+      if (a.status_dev) atomicExch(a.status_dev, SG_EINVAL);
+    }
+    return;
+  }
+  int32_t* nodes_out = a.accept_nodes_dev + static_cast<int64_t>(a.max_depth) * req;
+  for (int k = tid; k < a.max_depth; k += blockDim.x) nodes_out[k] = -1;
+  __syncthreads();
+  route_request<S>(a, req, r0, n, sh, true);
+  const int exit_row = sh.broken ? -1 : sh.lrow[sh.exit_node];
+  if (tid == 0) {
+    a.accept_len_dev[req] = sh.broken ? -1 : sh.depth;
+    if (a.terminal_leaf_dev)
+      a.terminal_leaf_dev[req] = (!sh.broken && exit_row < 0) ? sh.exit_node : -1;
+    if (sh.broken || exit_row < 0) a.bonus_dev[req] = -1;
+    if (sh.broken && a.status_dev) atomicExch(a.status_dev, SG_EINVAL);
+  }
+  if (a.keep_rows_dev) {
+    __syncthreads();  // nodes_out written by thread 0
+    int32_t* keep = a.keep_rows_dev + static_cast<int64_t>(a.max_depth + 1) * req;
+    for (int k = tid; k <= a.max_depth; k += blockDim.x)
+      keep[k] = (k == 0) ? 0 : (!sh.broken && k <= sh.depth ? nodes_out[k - 1] : -1);
+  }
+  if (sh.broken || exit_row < 0) return;
+  const int slabs = (a.vocab + kSlab - 1) / kSlab;
+  const float* __restrict__ src = slab_stats + static_cast<int64_t>(exit_row) * slabs * kSlabStats;
+  for (int k = tid; k < slabs; k += blockDim.x) {
+    s_m[k] = src[kSlabStats * k];
+    s_z[k] = src[kSlabStats * k + 1];
+    s_child_slab[k] = 0;
+  }
+  __syncthreads();
+  for (int k = tid; k < sh.child_count; k += blockDim.x) {
+    const int t = sh.child_tok[k];
+    if (t >= 0 && t < a.vocab) s_child_slab[t / kSlab] = 1;
+  }
+  __syncthreads();
+  const S* __restrict__ x = static_cast<const S*>(a.logits_dev) + a.logits_row_stride * exit_row;
+  // 1. complement sums of the slabs with child tokens
+  for (int s = wave; s < slabs; s += kWalkWaves) {
+    if (!s_child_slab[s]) continue;
+    float v[32];
+    load_slab<S, kVec>(x, a.vocab, s, lane, v);
+    const float z = slab_sum_skip(v, s_m[s], child_bits(sh.child_tok, sh.child_count, s, lane));
+    if (lane == 0) s_z[s] = z;
+  }
+  __syncthreads();
+  // 2. per-slab weights, then the sequential prefixes and the threshold
+  const float m_row = sh.rm[sh.exit_node];
+  for (int s = tid; s < slabs; s += blockDim.x) {
+    const float es = sg_exp_nonpos(s_m[s] - m_row);
+    s_es[s] = es;
+    s_w[s] = s_z[s] * es;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float p = 0.0f;
+    for (int s = 0; s < slabs; ++s) {
+      s_p[s] = p;
+      p = p + s_w[s];
+    }
+    s_thr = sh.u[2 * sh.depth + 1] * p;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  // 3. the crossing slab and token (every lane of wave 0 alike)
+  const float thr = s_thr;
+  int hit = -1;
+  for (int base = 0; base < slabs && hit < 0; base += kWave) {
+    const int s = base + lane;
+    const uint64_t mask = __ballot(s < slabs && s_p[s] + s_w[s] > thr);
+    if (mask != 0) hit = base + __builtin_ctzll(mask);
+  }
+  int bonus = -1;
+  if (hit >= 0) {
+    const float p = s_p[hit];
+    const float es = s_es[hit];
+    const float ms = s_m[hit];
+    float v[32];
+    load_slab<S, kVec>(x, a.vocab, hit, lane, v);
+    const uint32_t bits = child_bits(sh.child_tok, sh.child_count, hit, lane);
+    float q = 0.0f;
+    int candidate = INT_MAX;
+    int last = -1;
+#pragma unroll
+    for (int j = 0; j < kLinesPerSlab; ++j) {
+      const int t0 = hit * kSlab + kLine * j + 4 * lane;
+      float e[4];
+      bool nonchild[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        nonchild[c] = t0 + c < a.vocab && !((bits >> (4 * j + c)) & 1u);
+        e[c] = nonchild[c] ? sg_exp_nonpos(v[4 * j + c] - ms) : 0.0f;
+      }
+      float g = ((e[0] + e[1]) + e[2]) + e[3];
+#pragma unroll
+      for (int d = 1; d < kWave; d <<= 1) {
+        const float up = __shfl_up(g, d);
+        g = (lane >= d) ? g + up : g;
+      }
+      const float up = __shfl_up(g, 1);
+      float r = q + ((lane > 0) ? up : 0.0f);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        r = r + e[c];
+        if (nonchild[c] && candidate == INT_MAX && p + es * r > thr) candidate = t0 + c;
+        if (nonchild[c] && e[c] > 0.0f) last = t0 + c;
+      }
+      q = q + __shfl(g, kWave - 1);
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+      candidate = min(candidate, __shfl_xor(candidate, d));
+      last = max(last, __shfl_xor(last, d));
+    }
+    bonus = candidate != INT_MAX ? candidate : last;
+  } else {
+    // No slab crosses: the largest non-child token (every lane alike).
+    for (int t = a.vocab - 1; t >= 0; --t) {
+      bool child = false;
+      for (int k = 0; k < sh.child_count; ++k) child = child || sh.child_tok[k] == t;
+      if (!child) {
+        bonus = t;
+        break;
+      }
+    }
+  }
+  if (lane == 0) a.bonus_dev[req] = bonus;
+}
+
 __global__ void exp_probe_kernel(const float* __restrict__ x, float* __restrict__ out,
                                  int64_t count) {
   const int64_t k = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -760,7 +967,8 @@ void dispatch_logits(const void* p, int dtype, int64_t stride, int vocab, F&& f)
 }
 
 int launch_row_stats(const void* logits, int dtype, int64_t stride, int vocab, int rows,
-                     float* row_max, float* row_sum, int32_t* status, hipStream_t stream) {
+                     float* row_max, float* row_sum, float* slab_out, int32_t* status,
+                     hipStream_t stream) {
   if (rows == 0 && status == nullptr) return SG_OK;
   // One workgroup per row (one to clear the status when there are no rows).
   const dim3 grid(rows > 0 ? rows : 1);
@@ -768,7 +976,7 @@ int launch_row_stats(const void* logits, int dtype, int64_t stride, int vocab, i
     using S = decltype(elem);
     hipLaunchKernelGGL((row_stats_kernel<S, decltype(vec)::value>), grid, dim3(kStatsThreads),
                        0, stream, static_cast<const S*>(logits), stride, vocab, rows, row_max,
-                       row_sum, status);
+                       row_sum, slab_out, status);
   });
   SG_LAUNCH_CHECK();
   return SG_OK;
@@ -791,16 +999,29 @@ extern "C" int sg_row_stats(const void* logits_dev, int32_t logits_dtype, int64_
   SG_REQUIRE(num_rows == 0 || (logits_dev && row_max_dev && row_sum_dev),
              "null device pointer");
   return launch_row_stats(logits_dev, logits_dtype, row_stride, vocab, num_rows, row_max_dev,
-                          row_sum_dev, nullptr, reinterpret_cast<hipStream_t>(stream));
+                          row_sum_dev, nullptr, nullptr, reinterpret_cast<hipStream_t>(stream));
 }
 
-extern "C" int64_t sg_tree_sample_workspace_bytes(int32_t num_requests, int32_t vocab) {
-  using namespace sg;
-  if (num_requests < 0 || vocab < 1) return 0;
-  // Per request and slab: the slab's complement total and its line totals;
-  // then per request the record part 1 leaves for part 2.
+namespace sg {
+namespace {
+
+// Workspace layout: per request the complement draw's slab and line totals
+// and the record its two kernels pass on (SG_SAMPLE_STATS_READY calls), then
+// per statistics row its slab pairs (calls that compute statistics).
+int64_t request_region_floats(int num_requests, int vocab) {
   return static_cast<int64_t>(num_requests) *
-         (((vocab + kSlab - 1) / kSlab) * (1 + kLinesPerSlab) + kRecordInts) *
+         (((vocab + kSlab - 1) / kSlab) * (1 + kLinesPerSlab) + kRecordInts);
+}
+
+}  // namespace
+}  // namespace sg
+
+extern "C" int64_t sg_tree_sample_workspace_bytes(int32_t num_requests, int32_t num_rows,
+                                                  int32_t vocab) {
+  using namespace sg;
+  if (num_requests < 0 || num_rows < 0 || vocab < 1) return 0;
+  return (request_region_floats(num_requests, vocab) +
+          static_cast<int64_t>(num_rows) * ((vocab + kSlab - 1) / kSlab) * kSlabStats) *
          static_cast<int64_t>(sizeof(float));
 }
 
@@ -836,13 +1057,23 @@ int check_sample_args(const SgTreeSampleArgs* args) {
 }
 
 // Enqueues the three kernels of one sampling call; a.workspace_dev holds at
-// least sg_tree_sample_workspace_bytes(num_requests, vocab) bytes.
+// least sg_tree_sample_workspace_bytes(num_requests, statistics rows, vocab) bytes.
+int64_t stats_rows_of(const SgTreeSampleArgs& a) {
+  return (a.flags & SG_SAMPLE_STATS_READY) ? 0
+         : (a.num_logits_rows > 0 ? a.num_logits_rows : a.num_rows);
+}
+
 int launch_tree_sample(const SgTreeSampleArgs& a, hipStream_t s) {
-  // With SG_SAMPLE_STATS_READY the statistics pass only clears the status.
-  const int stats_rows = (a.flags & SG_SAMPLE_STATS_READY) ? 0
-                         : (a.num_logits_rows > 0 ? a.num_logits_rows : a.num_rows);
+  // With SG_SAMPLE_STATS_READY the statistics pass only clears the status and
+  // the complement draw runs (exit_totals + exit_find); otherwise the pass
+  // keeps every row's slab pairs and one kernel walks and draws.
+  const bool ready = (a.flags & SG_SAMPLE_STATS_READY) != 0;
+  const int stats_rows = static_cast<int>(stats_rows_of(a));
+  float* slab_stats = static_cast<float*>(a.workspace_dev) +
+                      request_region_floats(a.num_requests, a.vocab);
   int rc = launch_row_stats(a.logits_dev, a.logits_dtype, a.logits_row_stride, a.vocab,
-                            stats_rows, a.row_max_dev, a.row_sum_dev, a.status_dev, s);
+                            stats_rows, a.row_max_dev, a.row_sum_dev,
+                            ready ? nullptr : slab_stats, a.status_dev, s);
   if (rc != SG_OK) return rc;
   const int slabs = (a.vocab + kSlab - 1) / kSlab;
   const dim3 grid1(a.num_requests, (slabs + kWalkWaves - 1) / kWalkWaves);
@@ -851,6 +1082,12 @@ int launch_tree_sample(const SgTreeSampleArgs& a, hipStream_t s) {
                   [&](auto elem, auto vec) {
                     using S = decltype(elem);
                     constexpr bool kVec = decltype(vec)::value;
+                    if (!ready) {
+                      hipLaunchKernelGGL((slab_walk_kernel<S, kVec>), dim3(a.num_requests),
+                                         dim3(kWalkThreads), 0, s, a,
+                                         static_cast<const float*>(slab_stats));
+                      return;
+                    }
                     hipLaunchKernelGGL((exit_totals_kernel<S, kVec>), grid1, dim3(kWalkThreads),
                                        0, s, a);
                     err = hipGetLastError();
@@ -873,7 +1110,10 @@ extern "C" int sg_tree_sample(const SgTreeSampleArgs* args, sg_stream_t stream) 
   if (rc != SG_OK || args->num_requests == 0) return rc;
   const SgTreeSampleArgs& a = *args;
   SG_REQUIRE(a.workspace_dev != nullptr &&
-                 a.workspace_bytes >= sg_tree_sample_workspace_bytes(a.num_requests, a.vocab),
+                 static_cast<int64_t>(a.workspace_bytes) >=
+                     sg_tree_sample_workspace_bytes(a.num_requests,
+                                                    static_cast<int32_t>(stats_rows_of(a)),
+                                                    a.vocab),
              "workspace below sg_tree_sample_workspace_bytes");
   return launch_tree_sample(a, reinterpret_cast<hipStream_t>(stream));
 }
@@ -940,7 +1180,8 @@ extern "C" int sg_tree_sample_noalloc(const SgTreeSampleArgs* args, sg_stream_t 
   SG_REQUIRE(args->workspace_dev == nullptr && args->workspace_bytes == 0,
              "sg_tree_sample_noalloc uses its own scratch: workspace_dev must be NULL "
              "and workspace_bytes 0");
-  const int64_t need = sg_tree_sample_workspace_bytes(args->num_requests, args->vocab);
+  const int64_t need = sg_tree_sample_workspace_bytes(
+      args->num_requests, static_cast<int32_t>(stats_rows_of(*args)), args->vocab);
   if (need > static_cast<int64_t>(SG_TREE_SAMPLE_NOALLOC_SCRATCH_BYTES))
     return set_error(SG_EINVAL,
                      "sg_tree_sample_noalloc: " + std::to_string(args->num_requests) +

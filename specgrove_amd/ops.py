@@ -526,7 +526,9 @@ def tree_sample(logits: torch.Tensor, row_offset: torch.Tensor, parent: torch.Te
         )
     else:
         _check_sample_out(out, n, rows, max_depth)
-    ws_bytes = int(_lib.load().sg_tree_sample_workspace_bytes(n, logits.shape[1]))
+    # statistics of every logits row, with their slab pairs in the workspace
+    ws_bytes = int(_lib.load().sg_tree_sample_workspace_bytes(n, logits.shape[0],
+                                                              logits.shape[1]))
     if out.workspace is None or out.workspace.numel() < ws_bytes:
         out.workspace = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
     a = _sample_args(logits, row_offset, parent, token, uniforms, max_depth, out, n, rows,
@@ -596,7 +598,7 @@ def tree_sample_projected(logits: torch.Tensor, row_offset: torch.Tensor, parent
         _require(row_map.numel() == rows and row_map.is_contiguous(), "row_map must be [R]")
     dev = logits.device
     depth_slots = max(max_depth, 1)
-    ws_bytes = int(_lib.load().sg_tree_sample_workspace_bytes(n, logits.shape[1]))
+    ws_bytes = int(_lib.load().sg_tree_sample_workspace_bytes(n, 0, logits.shape[1]))
     out = ProjectedSampleResult(
         accept_nodes=torch.empty((n, depth_slots), dtype=torch.int32, device=dev),
         accept_len=torch.empty(n, dtype=torch.int32, device=dev),

@@ -20,7 +20,7 @@ def _declared_functions():
 
 def test_library_loads_and_struct_sizes_match():
     lib = _lib.load()
-    assert lib.sg_abi_version() == _lib.SG_ABI_VERSION == 4
+    assert lib.sg_abi_version() == _lib.SG_ABI_VERSION == 5
 
 
 def test_every_declared_symbol_is_exported():
@@ -176,7 +176,7 @@ def test_stale_plans_are_rejected_on_the_host():
 def test_noalloc_sampler_rejects_oversized_waves_before_any_device_call():
     lib = _lib.load()
     a = _lib.SgTreeSampleArgs()
-    per_request = lib.sg_tree_sample_workspace_bytes(1, 151936)
+    per_request = lib.sg_tree_sample_workspace_bytes(1, 1, 151936)  # one row each
     a.num_requests = _lib.NOALLOC_SCRATCH_BYTES // per_request + 1
     a.num_rows = a.num_requests
     a.vocab = 151936

@@ -258,3 +258,30 @@ def test_padded_logits_rows(device, oracle, dtype, vocab, pad):
     np.testing.assert_array_equal(res.accept_len.cpu().numpy(), length)
     np.testing.assert_array_equal(res.accept_nodes.cpu().numpy()[:, :case["max_depth"]], nodes)
     np.testing.assert_array_equal(res.bonus.cpu().numpy(), bonus)
+
+
+@pytest.mark.parametrize("vocab", [7, 2049, 4097, 6002, 151936])
+def test_slab_statistics_bit_exact(device, oracle, vocab):
+    """The statistics pass keeps every row's slab pairs (m_s, Z_s) behind the
+    per-request region of the workspace: bit for bit the oracle's, on the
+    vector path (vocab a multiple of 4) and the scalar one."""
+    rng = np.random.default_rng(vocab)
+    rows, n = 12, 3
+    logits = (rng.standard_normal((rows, vocab)) * 4).astype(np.float32)
+    logits[1, :vocab // 2] = -np.inf                 # slabs with no finite logit
+    case = dict(logits=logits, row_offset=np.array([0, 4, 8, 12], np.int32),
+                parent=np.tile(np.array([-1, 0, 0, 1], np.int32), 3),
+                token=np.tile(np.array([0, 1, 2, 3], np.int32) % vocab, 3),
+                uniforms=rng.random((n, 6), dtype=np.float32), max_depth=2)
+    t = {k: torch.from_numpy(case[k]).to(device)
+         for k in ("logits", "row_offset", "parent", "token", "uniforms")}
+    res = ops.tree_sample(t["logits"], t["row_offset"], t["parent"], t["token"],
+                          t["uniforms"], case["max_depth"])
+    slabs = (vocab + 2047) // 2048
+    request_floats = n * (slabs * 9 + 1028)
+    ws = res.workspace.view(torch.float32).cpu().numpy()
+    got = ws[request_floats:request_floats + rows * slabs * 2].reshape(rows, slabs, 2)
+    m, z, want = oracle.slab_stats(logits)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(res.row_sum.cpu().numpy().view(np.uint32), z.view(np.uint32))
+    _check_case(case, device, oracle)

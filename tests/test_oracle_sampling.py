@@ -194,3 +194,85 @@ def test_exp_coefficients_are_the_fitted_ones():
         got = [float.fromhex(re.search(rf"#define {prefix}{j} (\S+)f", text).group(1))
                for j in range(2, 6)]
         assert got == fitted, path
+
+
+@pytest.mark.parametrize("vocab", [7, 2049, 4096, 151936])
+def test_slab_stats_match_float64(oracle, vocab):
+    """Slab maxima exact; every 2048-token slab sum E(x - m_s) within float32
+    rounding of its float64 value; the row's Z their merged total."""
+    rng = np.random.default_rng(vocab + 1)
+    logits = (rng.standard_normal((3, vocab)) * np.array([[0.5], [3.0], [20.0]])).astype(
+        np.float32)
+    logits[0, :min(vocab, 2048)] = -np.inf       # a slab with no finite logit
+    m, z, ss = oracle.slab_stats(logits)
+    slabs = (vocab + 2047) // 2048
+    for r in range(3):
+        x = logits[r].astype(np.float64)
+        assert m[r] == logits[r].max()
+        for s in range(slabs):
+            seg = x[2048 * s:2048 * (s + 1)]
+            assert ss[r, s, 0] == np.float32(seg.max())
+            ref = np.exp(seg - seg.max()).sum() if np.isfinite(seg.max()) else 0.0
+            assert abs(ss[r, s, 1] - ref) <= 2e-6 * max(ref, 1e-30), (r, s)
+        total = sum(float(ss[r, s, 1]) * np.exp(float(ss[r, s, 0]) - float(m[r]))
+                    for s in range(slabs) if np.isfinite(ss[r, s, 0]))
+        assert abs(z[r] - total) <= 2e-5 * total
+        # the row statistics are the pass's own
+        assert (m[r], z[r]) == oracle.row_stats(logits[r])
+
+
+def test_slab_draw_matches_float64_inverse_cdf(oracle):
+    """Away from ties the slab draw is the float64 inverse-CDF token of the
+    complement, and it agrees with the complement draw."""
+    rng = np.random.default_rng(12)
+    vocab = 6001
+    mismatches = disagree = 0
+    trials = 1200
+    for k in range(trials):
+        row = (rng.standard_normal(vocab) * 3).astype(np.float32)
+        count = int(rng.integers(0, 6))
+        if k % 3 == 0:   # several children in one slab, one on a slab edge
+            base = 2048 * int(rng.integers(0, vocab // 2048))
+            children = np.unique(np.concatenate([[base, base + 2047],
+                                                 base + rng.integers(0, 2048, count)]))
+            children = children[children < vocab]
+        else:
+            children = rng.choice(vocab, size=count, replace=False)
+        row[children[:2]] += 4.0
+        u = np.float32(rng.random())
+        m, _, ss = oracle.slab_stats(row[None])
+        token, total = oracle.slab_draw(row, float(m[0]), ss[0], children, u)
+        e = np.exp(row.astype(np.float64) - float(m[0]))
+        e[children] = 0.0
+        c = np.cumsum(e)
+        thr = float(u) * c[-1]
+        expect = int(np.searchsorted(c, thr, side="right"))
+        assert token not in set(children.tolist()) and 0 <= token < vocab
+        assert abs(total - c[-1]) / c[-1] < 1e-5
+        if token != expect:
+            mismatches += 1
+            lo = min(token, expect)
+            assert abs(c[lo] - thr) / c[-1] < 1e-5
+        other, _ = oracle.complement_draw(row, float(m[0]), children, u)
+        disagree += other != token
+    assert mismatches <= trials // 200 and disagree <= trials // 200
+
+
+def test_slab_draw_fallbacks(oracle):
+    vocab = 600
+    row = np.full(vocab, -np.inf, np.float32)
+    row[[2, 599]] = 0.0                      # all mass on the two children
+    m, _, ss = oracle.slab_stats(row[None])
+    token, total = oracle.slab_draw(row, float(m[0]), ss[0], [2, 599], np.float32(0.3))
+    assert total == 0.0 and token == 598     # largest non-child token
+    flat = np.full(vocab, -np.inf, np.float32)
+    m, _, ss = oracle.slab_stats(flat[None])
+    assert oracle.slab_draw(flat, float(m[0]), ss[0], [], np.float32(0.5))[0] == vocab - 1
+    # u just below 1 lands on the last token with mass
+    row = np.zeros(vocab, np.float32)
+    row[vocab - 1] = -np.inf
+    m, _, ss = oracle.slab_stats(row[None])
+    token, _ = oracle.slab_draw(row, float(m[0]), ss[0], [5], np.float32(1.0 - 2 ** -24))
+    assert token == vocab - 2
+    token, _ = oracle.slab_draw(row, float(m[0]), ss[0], [0], np.float32(0.0))
+    assert token == 1

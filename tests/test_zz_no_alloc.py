@@ -71,7 +71,7 @@ def test_noalloc_matches_the_allocating_entry_point_twice(device, oracle):
 
 def test_noalloc_rejects_waves_beyond_its_scratch(device):
     vocab = 151936
-    per_request = int(_lib.load().sg_tree_sample_workspace_bytes(1, vocab))
+    per_request = int(_lib.load().sg_tree_sample_workspace_bytes(1, 1, vocab))  # one row each
     n = _lib.NOALLOC_SCRATCH_BYTES // per_request + 1
     logits = torch.zeros((n, vocab), dtype=torch.float32, device=device)
     row_offset = torch.arange(n + 1, dtype=torch.int32, device=device)
