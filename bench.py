@@ -8,12 +8,18 @@ value = packed rows / step time.  Inputs are resident in HBM; three distinct
 input sets (each with its own >1 GB KV cache) rotate so the 256 MB
 Infinity Cache cannot serve repeated reads.
 
+Every back-to-back figure is the median of 5 windows, each window K calls
+enqueued back to back between one pair of HIP events on the launch stream;
+the windows' own figures and the shader clock over each (a probe kernel on
+every XCD before and after the window) are reported beside it, and so is the
+clock over the per-call (event-bracketed) sequence.
+
 Also reported in the same JSON line:
-  roofline    the attention kernel: algorithmic bytes / the average of calls
-              enqueued back to back between one pair of HIP events on the
-              launch stream (as the step loop runs them);
+  step_timing the headline's windows and clocks;
+  roofline    the attention kernel: algorithmic bytes / its back-to-back time
+              (as the step loop runs it);
   attention   that back-to-back time, the per-call (event-bracketed) median,
-              rows/s, GB/s, TFLOP/s of visible-key flops;
+              windows and clocks, rows/s, GB/s, TFLOP/s of visible-key flops;
   commit      one-layer and whole 36-layer-stack commit calls;
   host        host (Python + ctypes) time to enqueue one step;
   qwen3_4b    the Qwen3-4B-shape wave (16 requests, 512 rows), 16 rotating
@@ -104,29 +110,60 @@ def _events(torch, n):
     return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
 
 
-def time_calls(torch, fn, iters):
-    """Per-call milliseconds from HIP events recorded on the current stream."""
+PROBE = None  # ops.ClockProbe on the launch stream, set in main()
+WINDOWS = 5   # back-to-back windows per figure; the figure is their median
+
+
+def _clock(a, b):
+    """Mean over XCDs of the average shader clock between two probe marks."""
+    if PROBE is None:
+        return None
+    per_xcd = list(PROBE.ghz(a, b).values())
+    return sum(per_xcd) / len(per_xcd) if per_xcd else None
+
+
+def time_calls(torch, fn, iters, record=None):
+    """Per-call milliseconds from HIP events recorded on the current stream
+    (each call bracketed by its own pair).  ``record`` (a dict), if given,
+    receives the shader clock over the whole sequence."""
     starts, ends = _events(torch, iters), _events(torch, iters)
     with gc_paused():
+        a = PROBE.mark() if PROBE is not None else None
         for k in range(iters):
             starts[k].record()
             fn(k)
             ends[k].record()
+        b = PROBE.mark() if PROBE is not None else None
         torch.cuda.synchronize()
+    if record is not None and a is not None:
+        record["clock_ghz_per_call"] = _clock(a, b)
     return [s.elapsed_time(e) for s, e in zip(starts, ends)]
 
 
-def back_to_back(torch, fn, iters):
-    """Average milliseconds per call of ``iters`` calls enqueued back to back
-    between one pair of HIP events on the current (launch) stream."""
-    start, end = _events(torch, 2)
+def back_to_back(torch, fn, iters, record=None, windows=WINDOWS):
+    """Milliseconds per call: the median over ``windows`` windows, each of
+    ``iters`` calls enqueued back to back between one pair of HIP events on
+    the current (launch) stream.  The call index runs on across windows, so
+    rotating input sets keep rotating.  ``record`` (a dict), if given,
+    receives every window's microseconds per call and its average shader
+    clock (probe kernels enqueued just outside each event pair)."""
+    evs = _events(torch, 2 * windows)
+    marks = []
     with gc_paused():
-        start.record()
-        for k in range(iters):
-            fn(k)
-        end.record()
+        for w in range(windows):
+            a = PROBE.mark() if PROBE is not None else None
+            evs[2 * w].record()
+            for k in range(iters):
+                fn(w * iters + k)
+            evs[2 * w + 1].record()
+            marks.append((a, PROBE.mark() if PROBE is not None else None))
         torch.cuda.synchronize()
-    return start.elapsed_time(end) / iters
+    per_window = [evs[2 * w].elapsed_time(evs[2 * w + 1]) / iters for w in range(windows)]
+    if record is not None:
+        record["windows_us"] = [round(v * 1e3, 2) for v in per_window]
+        if PROBE is not None:
+            record["clock_ghz"] = [round(_clock(a, b), 3) for a, b in marks]
+    return statistics.median(per_window)
 
 
 def build_attention_sets(torch, np, W, ops, device, steps_total, wl=None, sets=N_SETS):
@@ -169,8 +206,9 @@ def attention_line(torch, np, W, ops, device, wl, sets, iters, warmup):
     for k in range(warmup):
         call(k)
     torch.cuda.synchronize()
-    b2b = back_to_back(torch, call, iters)
-    per_call = time_calls(torch, call, iters)
+    timing: dict = {}
+    b2b = back_to_back(torch, call, iters, record=timing)
+    per_call = time_calls(torch, call, iters, record=timing)
     nbytes, flops = wl.algorithmic_bytes(), wl.algorithmic_flops()
     arena = sum(st["kc"].numel() * 2 * 2 for st in input_sets)
     del input_sets
@@ -181,6 +219,7 @@ def attention_line(torch, np, W, ops, device, wl, sets, iters, warmup):
                     f"{wl.num_q_heads}q/{wl.num_kv_heads}kv, D{wl.head_dim}",
         "input_sets": sets, "input_bytes": arena,
         "us_back_to_back": b2b * 1e3, "us_median_per_call": statistics.median(per_call) * 1e3,
+        **timing,
         "rows_per_s": wl.total_rows / (b2b * 1e-3),
         "gbs": nbytes / (b2b * 1e-3) / 1e9, "frac": nbytes / (b2b * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "tflops": flops / (b2b * 1e-3) / 1e12,
@@ -268,18 +307,12 @@ def commit_all_layers(torch, np, ops, wl, meta, device, layers=36, iters=50, war
     for k in range(warmup):
         call(k)
     torch.cuda.synchronize()
-    st, en = _events(torch, 2)
-    with gc_paused():
-        st.record()
-        for k in range(iters):
-            call(k)
-        en.record()
-        torch.cuda.synchronize()
-    us = st.elapsed_time(en) / iters * 1e3
+    us = back_to_back(torch, call, iters) * 1e3
     rows = int(sum(len(k) for k in wl.keep))
     del arena_k, arena_v, tree_k, tree_v
     return {"layers": layers, "us_per_call": us, "rows_per_layer": rows,
             "gbs": 2 * rows * hkv * d * 2 * 2 * layers / (us * 1e-6) / 1e9}
+
 
 def sampler_bench(torch, W, ops, device, iters, warmup, dtype=None):
     """The 64 x 32 x 151936 tree-sampling call over N_SETS rotating logits
@@ -305,10 +338,11 @@ def sampler_bench(torch, W, ops, device, iters, warmup, dtype=None):
     for k in range(warmup):
         call(k)
     torch.cuda.synchronize()
-    b2b = back_to_back(torch, call, iters)
-    ms = time_calls(torch, call, iters)
+    timing: dict = {}
+    b2b = back_to_back(torch, call, iters, record=timing)
+    ms = time_calls(torch, call, iters, record=timing)
     wl = sets[0]["wl"]
-    return wl, ms, sets, b2b
+    return wl, ms, sets, b2b, timing
 
 
 def layer_bench(torch, np, W, ops, device, iters=20, warmup=3):
@@ -539,8 +573,9 @@ def long_context_bench(torch, np, W, ops, device, iters=20, warmup=3):
     for k in range(warmup):
         attn(k)
     torch.cuda.synchronize()
-    attn_b2b = back_to_back(torch, attn, iters)
-    attn_ms = time_calls(torch, attn, iters)
+    lc_timing: dict = {}
+    attn_b2b = back_to_back(torch, attn, iters, record=lc_timing)
+    attn_ms = time_calls(torch, attn, iters, record=lc_timing)
     commit_ms = time_calls(torch, commit, iters)
     del q, kc, vc, kt, vt, out, ptrs
     torch.cuda.empty_cache()
@@ -574,6 +609,7 @@ def long_context_bench(torch, np, W, ops, device, iters=20, warmup=3):
                     f"({int(wl.prefix_len.sum())} tokens), {rows} rows, 32q/8kv, D128",
         "attention": {"us_back_to_back": attn_avg * 1e3,
                       "us_median_per_call": statistics.median(attn_ms) * 1e3,
+                      **lc_timing,
                       "rows_per_s": rows / (attn_avg * 1e-3),
                       "gbs": abytes / (attn_avg * 1e-3) / 1e9,
                       "frac": abytes / (attn_avg * 1e-3) / 1e9 / HBM_PEAK_GBS,
@@ -715,6 +751,8 @@ def main():
     if args.counters_only:
         counters_only(torch, np, W, ops, device, steps, warmup, args.counters_workload)
         return
+    global PROBE
+    PROBE = ops.ClockProbe(device, capacity=1024)
     wl, plan, meta, sets = build_attention_sets(torch, np, W, ops, device,
                                                 4 * (steps + warmup) + 16)
     rows = wl.total_rows
@@ -727,14 +765,8 @@ def main():
     for k in range(warmup):
         step(k)
     torch.cuda.synchronize()
-    start, end = _events(torch, 2)
-    with gc_paused():
-        start.record()
-        for k in range(steps):
-            step(k)
-        end.record()
-        torch.cuda.synchronize()
-    ms_per_step = start.elapsed_time(end) / steps
+    step_timing: dict = {}
+    ms_per_step = back_to_back(torch, step, steps, record=step_timing)
 
     # Host time to enqueue one step (argument checks, ctypes, launches); the
     # GPU runs behind, so this is the host's share, not the step's duration.
@@ -746,8 +778,9 @@ def main():
         torch.cuda.synchronize()
 
     attn_call = lambda k: attention_call(ops, wl, plan, meta, sets[k % N_SETS])  # noqa: E731
-    attn_b2b = back_to_back(torch, attn_call, steps)
-    attn_ms = time_calls(torch, attn_call, steps)
+    attn_timing: dict = {}
+    attn_b2b = back_to_back(torch, attn_call, steps, record=attn_timing)
+    attn_ms = time_calls(torch, attn_call, steps, record=attn_timing)
     commit_one = lambda k: commit_call(ops, wl, meta, sets[k % N_SETS])  # noqa: E731
     commit_b2b = back_to_back(torch, commit_one, steps)
     commit_ms = time_calls(torch, commit_one, steps)
@@ -764,6 +797,8 @@ def main():
         "steps": steps,
         "warmup": warmup,
         "ms_per_step": ms_per_step,
+        "step_timing": dict(step_timing, rule=f"median of {WINDOWS} windows of {steps} steps "
+                            "back to back (each window between one pair of HIP events)"),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -788,11 +823,13 @@ def main():
             "traffic_source": traffic_source,
             "kernel": "sg_tree_attn_fwd (tree_attn_kernel<128> + merge)",
             "algorithmic_bytes": attn_bytes,
-            "timing": f"{steps} calls back to back between one pair of HIP events",
+            "timing": f"median of {WINDOWS} windows of {steps} calls back to back, each "
+                      "between one pair of HIP events on the launch stream",
         },
         "attention": {
             "us_back_to_back": attn_b2b * 1e3,
             "us_median_per_call": statistics.median(attn_ms) * 1e3,
+            **attn_timing,
             "rows_per_s": rows / (attn_b2b * 1e-3),
             "gbs": achieved,
             "tflops": attn_flops / (attn_b2b * 1e-3) / 1e12,
@@ -820,12 +857,14 @@ def main():
 
     samp_sets = None
     if not args.no_sampler:
-        swl, samp_ms, samp_sets, samp_b2b = sampler_bench(torch, W, ops, device, steps, warmup)
+        swl, samp_ms, samp_sets, samp_b2b, samp_timing = sampler_bench(torch, W, ops, device,
+                                                                        steps, warmup)
         sbytes = swl.algorithmic_bytes()
         result["sampler"] = {
             "workload": swl.name,
             "us_back_to_back": samp_b2b * 1e3,
             "us_median_per_call": statistics.median(samp_ms) * 1e3,
+            **samp_timing,
             "nodes_per_s": swl.total_rows / (samp_b2b * 1e-3),
             "gbs": sbytes / (samp_b2b * 1e-3) / 1e9,
             "frac": sbytes / (samp_b2b * 1e-3) / 1e9 / HBM_PEAK_GBS,
@@ -833,8 +872,8 @@ def main():
         }
         # The same call on bf16 logits (what the LM head writes): half the
         # bytes, the same decisions as on their fp32 widening.
-        _, bf_ms, bf_sets, bf_b2b = sampler_bench(torch, W, ops, device, steps, warmup,
-                                                  dtype=torch.bfloat16)
+        _, bf_ms, bf_sets, bf_b2b, bf_timing = sampler_bench(torch, W, ops, device, steps,
+                                                             warmup, dtype=torch.bfloat16)
         del bf_sets
         torch.cuda.empty_cache()
         bbytes = sbytes // 2
@@ -842,6 +881,7 @@ def main():
             "workload": swl.name + " (bf16 logits)",
             "us_back_to_back": bf_b2b * 1e3,
             "us_median_per_call": statistics.median(bf_ms) * 1e3,
+            **bf_timing,
             "nodes_per_s": swl.total_rows / (bf_b2b * 1e-3),
             "gbs": bbytes / (bf_b2b * 1e-3) / 1e9,
             "frac": bbytes / (bf_b2b * 1e-3) / 1e9 / HBM_PEAK_GBS,

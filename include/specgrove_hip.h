@@ -444,6 +444,17 @@ int sg_gather_rows(const void* const* src_dev, int32_t num_src, int64_t src_row_
  * Returns -1 for an unknown index.  No reference counterpart. */
 int64_t sg_abi_struct_size(int32_t which);
 
+/* Measurement helper, no reference counterpart: each of `blocks` workgroups
+ * writes four int64 to out_dev[4*b ..]: the XCD it ran on, the shader-clock
+ * counter, the constant-rate wall-clock counter, and its hardware id (CU,
+ * array and engine).  Two probes bracketing a timed region give, per CU that
+ * both saw, its average shader clock over the region. */
+int sg_clock_probe(int64_t* out_dev, int32_t blocks, sg_stream_t stream);
+
+/* Rate of the wall-clock counter sg_clock_probe samples, in kHz (-1 on error).
+ * No reference counterpart. */
+int64_t sg_wall_clock_khz(int32_t device);
+
 /* Test hook: E(x) of the sampler's exp for count values (device arrays). */
 int sg_exp_probe(const float* x_dev, float* out_dev, int64_t count,
                  sg_stream_t stream);

@@ -135,6 +135,7 @@ EXPORTED_SYMBOLS = (
     "sg_abi_version", "sg_last_error", "sg_abi_struct_size",
     "sg_tree_attn_plan", "sg_tree_attn_fwd", "sg_kv_commit",
     "sg_tree_sample", "sg_tree_sample_workspace_bytes", "sg_row_stats", "sg_exp_probe",
+    "sg_clock_probe", "sg_wall_clock_khz",
     "sg_tree_sample_noalloc", "sg_tree_attn_plan_check", "sg_kv_split",
     "sg_lm_head", "sg_lm_head_tile_count", "sg_lm_head_packed", "sg_lm_head_pack_weight",
     "sg_lm_head_packed_bytes",
@@ -209,6 +210,10 @@ def load() -> ctypes.CDLL:
     lib.sg_gather_rows.restype = c_i32
     lib.sg_gather_rows.argtypes = [c_void_p, c_i32, c_i64, c_i32, c_i32, c_void_p, c_i32,
                                    c_void_p, c_i64, c_void_p, c_void_p]
+    lib.sg_clock_probe.restype = c_i32
+    lib.sg_clock_probe.argtypes = [c_void_p, c_i32, c_void_p]
+    lib.sg_wall_clock_khz.restype = c_i64
+    lib.sg_wall_clock_khz.argtypes = [c_i32]
     lib.sg_exp_probe.restype = c_i32
     lib.sg_exp_probe.argtypes = [c_void_p, c_void_p, c_i64, c_void_p]
     version = lib.sg_abi_version()

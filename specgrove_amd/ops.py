@@ -640,6 +640,58 @@ def exp_probe(x: torch.Tensor) -> torch.Tensor:
     return out
 
 
+class ClockProbe:
+    """Average shader clock over timed regions, per XCD.
+
+    ``mark()`` enqueues ``sg_clock_probe`` on the current stream and returns
+    the mark's index; after the stream has been synchronized, ``ghz(a, b)``
+    gives {xcd: GHz} between marks ``a`` and ``b``.  The shader-cycle counters
+    of different CUs are not aligned, so every CU that both marks saw gives
+    its own clock (its counter's delta over the constant-rate counter's delta,
+    times that counter's rate) and each XCD reports the median over its CUs.
+    ``blocks`` workgroups per mark (1,024: every CU is seen by nearly every
+    mark).  ``spread(a)`` is the largest difference of the shader-cycle
+    counter between workgroups on one CU at one mark.
+    """
+
+    def __init__(self, device, capacity: int = 512, blocks: int = 1024):
+        lib = _lib.load()
+        index = torch.device(device).index or 0
+        khz = int(lib.sg_wall_clock_khz(index))
+        _require(khz > 0, "sg_wall_clock_khz failed: "
+                 + lib.sg_last_error().decode(errors="replace"))
+        self.wall_hz = khz * 1e3
+        self.blocks, self.capacity, self.count = blocks, capacity, 0
+        self._buf = torch.zeros((capacity, blocks, 4), dtype=torch.int64, device=device)
+
+    def mark(self) -> int:
+        _require(self.count < self.capacity, "clock probe capacity exhausted")
+        _lib.check(_lib.load().sg_clock_probe(self._buf[self.count].data_ptr(), self.blocks,
+                                              _stream_handle()), "sg_clock_probe")
+        self.count += 1
+        return self.count - 1
+
+    def _per_cu(self, mark: int) -> dict:
+        h = self._buf[mark].cpu().numpy()
+        keys = h[:, 0] * 256 + ((h[:, 3] >> 8) & 0xFF)  # XCD, engine, array, CU
+        return {int(k): (np.median(h[keys == k][:, 1]), np.median(h[keys == k][:, 2]),
+                         int(np.ptp(h[keys == k][:, 1])))
+                for k in np.unique(keys)}
+
+    def ghz(self, a: int, b: int) -> dict:
+        ra, rb = self._per_cu(a), self._per_cu(b)
+        per_xcd: dict = {}
+        for k in ra.keys() & rb.keys():
+            ticks = rb[k][1] - ra[k][1]
+            if ticks > 0:
+                per_xcd.setdefault(k // 256, []).append(
+                    (rb[k][0] - ra[k][0]) / ticks * self.wall_hz / 1e9)
+        return {x: float(np.median(v)) for x, v in sorted(per_xcd.items())}
+
+    def spread(self, a: int) -> int:
+        return max(v[2] for v in self._per_cu(a).values())
+
+
 # --------------------------------------------------------------------------
 # (D) LM head with fused statistics
 # --------------------------------------------------------------------------
