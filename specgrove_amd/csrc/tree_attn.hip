@@ -851,15 +851,19 @@ __global__ __launch_bounds__(kThreads, kListsPerCU) void tree_attn_kernel(SgTree
 }
 
 // Combines the partials of the split groups: merge_blocks_per_group(D)
-// workgroups per group, thread -> one (query vector, float4 chunk).
+// workgroups per group, thread -> one (query vector, float4 chunk).  groups:
+// the plan's merge-group records on the device when the host knows where they
+// are (saves the round trip through the plan header), else nullptr.
 template <int D>
-__global__ __launch_bounds__(kMergeThreads) void tree_attn_merge_kernel(SgTreeAttnArgs a) {
-  const PlanHeader* hdr = static_cast<const PlanHeader*>(a.plan_dev);
-  constexpr int CH = D / 4;  // float4 chunks per query vector
+__global__ __launch_bounds__(kMergeThreads) void tree_attn_merge_kernel(
+    SgTreeAttnArgs a, const MergeGroup* groups) {
+  if (groups == nullptr) {
+    const PlanHeader* hdr = static_cast<const PlanHeader*>(a.plan_dev);
+    groups = reinterpret_cast<const MergeGroup*>(reinterpret_cast<const AttnUnit*>(hdr + 1) +
+                                                 hdr->num_units);
+  }
   const int sub = blockIdx.x % merge_blocks_per_group(D);
-  const MergeGroup grp = reinterpret_cast<const MergeGroup*>(
-      reinterpret_cast<const AttnUnit*>(hdr + 1) +
-      hdr->num_units)[blockIdx.x / merge_blocks_per_group(D)];
+  const MergeGroup grp = groups[blockIdx.x / merge_blocks_per_group(D)];
   const int G = a.num_q_heads / a.num_kv_heads;
   const int r0 = a.row_offset_dev[grp.req];
   const float* ws = static_cast<const float*>(a.workspace_dev);
@@ -1243,9 +1247,13 @@ extern "C" int sg_tree_attn_fwd(const SgTreeAttnArgs* args, sg_stream_t stream) 
   SG_REQUIRE(a.head_dim == 64 || a.head_dim == 128, "head_dim must be 64 or 128");
   SG_REQUIRE(a.num_requests >= 0 && a.num_rows >= 0, "negative sizes");
   SG_REQUIRE(a.plan_units >= 0 && a.plan_merges >= 0, "negative plan sizes");
+  const MergeGroup* merge_groups = nullptr;
   if (a.plan_host != nullptr) {
     PlanHeader hdr;
     std::memcpy(&hdr, a.plan_host, sizeof(hdr));
+    merge_groups = reinterpret_cast<const MergeGroup*>(
+        static_cast<const char*>(a.plan_dev) + sizeof(PlanHeader) +
+        sizeof(AttnUnit) * static_cast<size_t>(hdr.num_units));
     SG_REQUIRE(hdr.magic == kPlanMagic, "plan_host is not a plan of sg_tree_attn_plan");
     SG_REQUIRE(hdr.group == G && hdr.head_dim == a.head_dim &&
                    hdr.num_kv_heads == a.num_kv_heads,
@@ -1281,7 +1289,7 @@ extern "C" int sg_tree_attn_fwd(const SgTreeAttnArgs* args, sg_stream_t stream) 
     if (a.plan_merges > 0) {
       hipLaunchKernelGGL(tree_attn_merge_kernel<128>,
                          dim3(a.plan_merges * merge_blocks_per_group(128)), dim3(kMergeThreads),
-                         0, s, a);
+                         0, s, a, merge_groups);
       SG_LAUNCH_CHECK();
     }
   } else {
@@ -1290,7 +1298,7 @@ extern "C" int sg_tree_attn_fwd(const SgTreeAttnArgs* args, sg_stream_t stream) 
     if (a.plan_merges > 0) {
       hipLaunchKernelGGL(tree_attn_merge_kernel<64>,
                          dim3(a.plan_merges * merge_blocks_per_group(64)), dim3(kMergeThreads),
-                         0, s, a);
+                         0, s, a, merge_groups);
       SG_LAUNCH_CHECK();
     }
   }
