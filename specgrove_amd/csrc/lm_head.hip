@@ -10,9 +10,12 @@
 // the tree walk routes with, so no separate pass reads the logits to normalise
 // them.
 //
-// Kernel (one 4-wave workgroup per CU, 1 wave per SIMD):
-//   tile      = 256 vocabulary tokens x 256 projected rows; wave w owns the
-//               128 x 128 quarter (tokens 128*(w&1).., rows 128*(w>>1)..);
+// Kernels: lm_head_pp_kernel for more than 128 projected rows (eight waves
+// in two groups that alternate between the matrix pipe and the LDS/copy
+// pipes, described at the kernel), lm_head_kernel<R> for up to 128 rows and
+// for hidden sizes of 64 (one 4-wave workgroup per CU, 1 wave per SIMD):
+//   tile      = 256 vocabulary tokens x 64 R projected rows; wave w owns the
+//               128 x 32 R quarter (tokens 128*(w&1).., rows 32 R (w>>1)..);
 //   ring      = four stages of 32 hidden dims: the weight and hidden chunks
 //               move HBM -> LDS with global_load_lds_dwordx4 (no register
 //               staging), 64 contiguous bytes of each row per copy lane
@@ -67,8 +70,9 @@ constexpr int kLmXcds = 8;
 constexpr int kMergeRowsPerBlock = 4;   // rows per 256-thread merge workgroup
 
 // Row tile of R 32-row blocks per wave (64*R projected rows per workgroup):
-// R = 4 for waves of more than 128 rows, 2 up to 128, 1 up to 64 (the leaf
-// pass), so a small call does not multiply empty rows.
+// R = 2 up to 128 rows, 1 up to 64 (the leaf pass), so a small call does not
+// multiply empty rows; R = 4 only where the ping-pong kernel cannot run (a
+// hidden size of 64, two stages).
 template <int R>
 struct RowTile {
   static constexpr int kRows = 64 * R;
@@ -426,6 +430,276 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
   }
 }
 
+// Ping-pong form of the 256-row tile (more than 128 projected rows): eight
+// waves, two per SIMD, in two groups (waves 0-3 and 4-7) half a stage apart.
+// Wave w owns tokens [128*(w&1), +128) and rows [64*(2*(w>>2) + ((w>>1)&1)),
+// +64) of the 256 x 256 tile: 4 x 2 blocks of 32 x 32, 128 accumulators.  In
+// phase 2t group A (waves 0-3) reads stage t's fragments from LDS and issues
+// its share of the copies of stage t+3 while group B multiplies stage t-1; in
+// phase 2t+1 the groups swap roles.  The two waves of a SIMD thus alternate
+// between the matrix pipe and the LDS/copy pipes instead of meeting at the
+// same barrier with the same work.  One barrier per phase; before it every
+// wave waits for its own copies of the stage the next phase reads.  The
+// products, their order per accumulator (ascending hidden dims) and the
+// epilogue's statistics order are those of lm_head_kernel, so the logits and
+// statistics are bit-identical.
+constexpr int kPpThreads = 512;
+struct PpTile {
+  static constexpr int kRows = 256;
+  static constexpr int kXBytes = kRows * kStepK * 2;  // hidden bytes per stage (16 KiB)
+  static constexpr int kStage = kWBytes + kXBytes;     // 32 KiB
+  static constexpr int kDmas = 4;                      // copies per wave per stage
+  static constexpr int kStaging = 8 * 64 * kOutPitch;  // 64 rows x 128 tokens per wave
+  static constexpr int kLds = kLmStages * kStage > kStaging ? kLmStages * kStage : kStaging;
+};
+
+template <bool kPacked>
+__global__ __launch_bounds__(kPpThreads, 1) void lm_head_pp_kernel(SgLmHeadArgs a, int v_tiles,
+                                                                    int r_tiles) {
+  using T = PpTile;
+  __shared__ __align__(1024) unsigned char smem[T::kLds];
+  int vt, rt;
+  if (!tile_of(blockIdx.x, v_tiles, r_tiles, vt, rt)) return;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2;               // 0: group A, 1: group B
+  const int wv = wave & 1;                 // 128-token half of the tile
+  const int wr = 2 * grp + ((wave >> 1) & 1);  // 64-row quarter of the tile
+  const int half = lane >> 5;
+  const int col = lane & 31;
+  const int V = a.vocab;
+  const int v0 = vt * kTileV;
+  const int r0 = rt * T::kRows;
+
+  // Copy slots, with the operand stage layout of lm_head_kernel: weight copy q
+  // (rows 16q .. 16q+15, 64 bytes each) at LDS 1024 q, hidden copy q at
+  // kWBytes + 1024 q; wave w issues weight and hidden copies 2w and 2w+1.
+  uint32_t w_off[2], w_lds[2], x_off[2], x_lds[2];
+  const int steps = a.hidden_size / kStepK;
+  const unsigned char* wbase =
+      static_cast<const unsigned char*>(a.weight_dev) +
+      (kPacked ? static_cast<int64_t>(vt) * steps * kWBytes
+               : static_cast<int64_t>(v0) * a.weight_row_stride * 2);
+  constexpr int64_t kWStep = kPacked ? kWBytes : kStepK * 2;
+  const unsigned char* xbase = static_cast<const unsigned char*>(a.hidden_dev);
+  bool bad_index = false;
+  const int g_lane = (lane & 3) ^ ((lane >> 4) & 3);  // swz(row) = (row >> 2) & 3
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int q = 2 * wave + i;
+    const int row = 16 * q + (lane >> 2);
+    const int dim = 8 * g_lane;
+    const int tok = min(v0 + row, V - 1) - v0;
+    w_off[i] = kPacked ? static_cast<uint32_t>(row * kStepK * 2 + dim * 2)
+                       : static_cast<uint32_t>((static_cast<int64_t>(tok) * a.weight_row_stride +
+                                                dim) * 2);
+    w_lds[i] = static_cast<uint32_t>(1024 * q);
+    const int prow = min(r0 + row, a.num_rows - 1);
+    int src = a.row_index_dev != nullptr ? a.row_index_dev[prow] : prow;
+    if (src < 0 || src >= a.num_hidden_rows) {
+      bad_index = bad_index || (r0 + row < a.num_rows);
+      src = 0;
+    }
+    x_off[i] = static_cast<uint32_t>((static_cast<int64_t>(src) * a.hidden_row_stride + dim) * 2);
+    x_lds[i] = static_cast<uint32_t>(kWBytes + 1024 * q);
+  }
+  if (bad_index && a.status_dev != nullptr) atomicExch(a.status_dev, SG_EINVAL);
+
+  const uint32_t ring = lds_addr(smem);
+  auto issue = [&](int t) {
+    const uint32_t stage = ring + (t % kLmStages) * T::kStage;
+    const unsigned char* wk = wbase + static_cast<int64_t>(t) * kWStep;
+    const unsigned char* xk = xbase + static_cast<int64_t>(t) * kStepK * 2;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) dma16(wk, w_off[i], stage + w_lds[i]);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) dma16(xk, x_off[i], stage + x_lds[i]);
+  };
+
+  int lp[2];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+    lp[kb] = (lane & 31) * 64 + 16 * ((2 * kb + (lane >> 5)) ^ (((lane & 31) >> 2) & 3));
+  const int a_base = wv * 4 * 2048;
+  const int b_base = kWBytes + wr * 2 * 2048;
+  // Waits until at most `newer` stages of this wave's copies are in flight.
+  auto wait_newer = [&](int newer) {
+    if (newer >= 2) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_encoding(2 * T::kDmas));
+    } else if (newer == 1) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_encoding(T::kDmas));
+    } else {
+      __builtin_amdgcn_s_waitcnt(vmcnt_encoding(0));
+    }
+  };
+  for (int t = 0; t < kLmStages - 1 && t < steps; ++t) issue(t);
+  wait_newer(min(kLmStages - 2, steps - 1));  // stage 0 has landed
+  __syncthreads();
+
+  // The main loop and the epilogue, once per group (G known at compile time,
+  // so each copy is straight-line code with one product site).  A barrier
+  // counts arrivals, not instructions: both copies pass 2 steps + 1 barriers.
+  // Group A: phase 2t reads stage t and issues stage t+3, phase 2t+1
+  // multiplies.  Group B: one idle phase, then phase 2t+1 reads stage t and
+  // issues stage t+3, phase 2t+2 multiplies.  Before the barrier that ends
+  // phase p every wave waits for its own copies of the stage read in phase
+  // p+1, so that the barrier publishes the whole stage.
+  auto body = [&](auto group) {
+    constexpr int G = decltype(group)::value;
+    floatx16 acc[4][2];
+#pragma unroll
+    for (int vb = 0; vb < 4; ++vb)
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[vb][rb][r] = 0.0f;
+    bf16x8 fw[2][4], fx[2][2];
+    auto read_frags = [&](int t) {
+      const unsigned char* st = smem + (t % kLmStages) * T::kStage;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int vb = 0; vb < 4; ++vb)
+          fw[kb][vb] = as_bf16x8(*reinterpret_cast<const uint4*>(st + a_base + vb * 2048 + lp[kb]));
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+          fx[kb][rb] = as_bf16x8(*reinterpret_cast<const uint4*>(st + b_base + rb * 2048 + lp[kb]));
+      }
+    };
+    auto mma = [&]() {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int vb = 0; vb < 4; ++vb)
+#pragma unroll
+          for (int rb = 0; rb < 2; ++rb)
+            acc[vb][rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fw[kb][vb], fx[kb][rb],
+                                                                  acc[vb][rb], 0, 0, 0);
+    };
+    // One stage: read its fragments (and issue stage t+3 while steps remain),
+    // multiply.  N is the number of this wave's stages newer than t+1 that
+    // may stay in flight once stage t+1 must have landed (-1: t is the last
+    // stage); a constant, so that the wait stays where it is written.
+    auto stage_step = [&](int t, auto newer) {
+      constexpr int N = decltype(newer)::value;
+      auto wait_next = [&]() {
+        if constexpr (N >= 2) {
+          __builtin_amdgcn_s_waitcnt(vmcnt_encoding(2 * T::kDmas));
+        } else if constexpr (N == 1) {
+          __builtin_amdgcn_s_waitcnt(vmcnt_encoding(T::kDmas));
+        } else if constexpr (N == 0) {
+          __builtin_amdgcn_s_waitcnt(vmcnt_encoding(0));
+        }
+      };
+      read_frags(t);
+      if constexpr (N >= 2) issue(t + kLmStages - 1);
+      // A: the next phase is B's read of stage t (landed).  B: the next phase
+      // is A's read of stage t+1.
+      if constexpr (G == 1) wait_next();
+      // The scheduling fences keep every product inside its phase (the
+      // compiler may otherwise move them across the barriers).
+      __builtin_amdgcn_sched_barrier(0);
+      __syncthreads();
+      __builtin_amdgcn_sched_barrier(0);
+      mma();
+      __builtin_amdgcn_sched_barrier(0);
+      // A: the next phase reads stage t+1.  B: the next phase is B's read of
+      // stage t+1, landed before the barrier above.
+      if constexpr (G == 0) wait_next();
+      __builtin_amdgcn_sched_barrier(0);
+      __syncthreads();
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    static_assert(kLmStages == 4, "the tail below is written for a four-stage ring");
+    if constexpr (G == 1) __syncthreads();  // phase 0: group A reads stage 0
+    // steps >= 3 (the launcher's condition); stage t+3 exists for t < steps-3.
+    for (int t = 0; t + kLmStages - 1 < steps; ++t) stage_step(t, std::integral_constant<int, 2>{});
+    stage_step(steps - 3, std::integral_constant<int, 1>{});
+    stage_step(steps - 2, std::integral_constant<int, 0>{});
+    stage_step(steps - 1, std::integral_constant<int, -1>{});
+    if constexpr (G == 0) __syncthreads();  // phase 2 steps: B's last products
+    // The ring is free (every barrier above waited for the LDS reads): it
+    // becomes the output staging area.
+
+    // Epilogue (lm_head_kernel's, for 2 row blocks): acc[vb][rb][r] holds token
+    // v0 + 128*wv + 32*vb + 8*(r/4) + 4*half + r%4 of tile row 64*wr + 32*rb + col.
+    const int tok0 = v0 + 128 * wv;
+    const bool tile_live = tok0 < V;
+    const int n_tiles = (V + kStatTokens - 1) / kStatTokens;
+    unsigned char* stage = smem + wave * 64 * kOutPitch;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const int row_local = 32 * rb + col;
+      const int row = r0 + 64 * wr + row_local;
+      float x[64];
+      float m = -__builtin_inff();
+#pragma unroll
+      for (int vb = 0; vb < 4; ++vb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int tok = tok0 + 32 * vb + 8 * (r >> 2) + 4 * half + (r & 3);
+          x[16 * vb + r] = bf16_to_f32(f32_to_bf16(acc[vb][rb][r]));
+          m = (tok < V) ? fmaxf(m, x[16 * vb + r]) : m;
+        }
+      m = half_max(m);
+      const float mc = (m == -__builtin_inff()) ? 0.0f : m;
+      float z = 0.0f;
+#pragma unroll
+      for (int vb = 0; vb < 4; ++vb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int tok = tok0 + 32 * vb + 8 * (r >> 2) + 4 * half + (r & 3);
+          const float e = sg_exp_nonpos(x[16 * vb + r] - mc);
+          z = z + ((tok < V) ? e : 0.0f);
+        }
+      z = half_sum(z);
+      if (half == 0 && tile_live && row < a.num_rows) {
+        float* dst =
+            a.tile_stats_dev + (static_cast<int64_t>(row) * n_tiles + tok0 / kStatTokens) * 2;
+        *reinterpret_cast<float2*>(dst) = make_float2(m, z);
+      }
+#pragma unroll
+      for (int vb = 0; vb < 4; ++vb)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          uint2 packed;
+          packed.x = pack_bf16x2(x[16 * vb + 4 * q], x[16 * vb + 4 * q + 1]);
+          packed.y = pack_bf16x2(x[16 * vb + 4 * q + 2], x[16 * vb + 4 * q + 3]);
+          *reinterpret_cast<uint2*>(stage + row_local * kOutPitch +
+                                    2 * (32 * vb + 8 * q + 4 * half)) = packed;
+        }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (!tile_live) return;
+    uint16_t* out = static_cast<uint16_t*>(a.logits_dev);
+#pragma unroll 4
+    for (int i = 0; i < 16; ++i) {
+      const int row_local = 4 * i + (lane >> 4);
+      const int row = r0 + 64 * wr + row_local;
+      const int chunk = lane & 15;
+      const int tok = tok0 + 8 * chunk;
+      const uint4 v = *reinterpret_cast<const uint4*>(stage + row_local * kOutPitch + 16 * chunk);
+      if (row >= a.num_rows || tok >= V) continue;
+      uint16_t* dst = out + static_cast<int64_t>(row) * a.logits_row_stride + tok;
+      if (tok + 8 <= V) {
+        *reinterpret_cast<uint4*>(dst) = v;
+      } else {
+        for (int e = 0; tok + e < V; ++e) {
+          const uint32_t w = (e >> 1) == 0 ? v.x : (e >> 1) == 1 ? v.y : (e >> 1) == 2 ? v.z : v.w;
+          dst[e] = static_cast<uint16_t>((e & 1) ? (w >> 16) : (w & 0xffffu));
+        }
+      }
+    }
+  };
+  if (grp == 0) {
+    body(std::integral_constant<int, 0>{});
+  } else {
+    body(std::integral_constant<int, 1>{});
+  }
+}
+
 // Row (max, sum) from the tile pairs: one wave per row; lane l merges tiles
 // l, l+64, ... in increasing order, then the xor butterfly merges the lanes.
 __global__ __launch_bounds__(kMergeRowsPerBlock * kWave) void lm_head_rows_kernel(SgLmHeadArgs a) {
@@ -518,8 +792,26 @@ int launch_lm_head(const SgLmHeadArgs& a, bool packed, hipStream_t s) {
     SG_LAUNCH_CHECK();
     return SG_OK;
   };
+  auto launch_pp = [&]() -> int {
+    const int r_tiles = (a.num_rows + PpTile::kRows - 1) / PpTile::kRows;
+    const int64_t blocks =
+        static_cast<int64_t>((v_tiles + kLmXcds - 1) / kLmXcds) * kLmXcds * r_tiles;
+    SG_REQUIRE(blocks < INT32_MAX, "wave too large");
+    if (packed) {
+      lm_head_pp_kernel<true><<<dim3(static_cast<unsigned>(blocks)), dim3(kPpThreads), 0, s>>>(
+          a, v_tiles, r_tiles);
+    } else {
+      lm_head_pp_kernel<false><<<dim3(static_cast<unsigned>(blocks)), dim3(kPpThreads), 0, s>>>(
+          a, v_tiles, r_tiles);
+    }
+    SG_LAUNCH_CHECK();
+    return SG_OK;
+  };
+  // The ping-pong kernel's straight-line tail needs three stages or more.
+  const bool pp = a.hidden_size / kStepK >= kLmStages - 1;
   const int rc = a.num_rows <= 64    ? launch(std::integral_constant<int, 1>{})
                  : a.num_rows <= 128 ? launch(std::integral_constant<int, 2>{})
+                 : pp                ? launch_pp()
                                      : launch(std::integral_constant<int, 4>{});
   if (rc != SG_OK) return rc;
   const int merge_blocks = (a.num_rows + kMergeRowsPerBlock - 1) / kMergeRowsPerBlock;
