@@ -121,6 +121,71 @@ __device__ __forceinline__ float half_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Two fp32 values to a packed bf16 pair (low half: lo), nearest-even
+// rounding by v_cvt_pk_bf16_f32; for the finite values this library rounds
+// it equals f32_to_bf16 bit for bit.
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
+  typedef __attribute__((ext_vector_type(2))) float f32x2;
+  typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+  const f32x2 f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+}
+
+// Epilogue of one 32-row block of a wave's 128-token statistics tile.  The
+// lane's accumulators acc[vb][rb] hold row `col` of the block at tokens
+// tok0 + 32 vb + 8 (r/4) + 4 half + r%4 (element r).  Rounds them to bf16,
+// writes the bf16 logits into the lane's staging row (128 tokens) and
+// returns the tile's (m, z) of the statistics contract: m the maximum, z the
+// sum of E(x - m) in increasing (vb, r) per half, then z_0 + z_1.  kFull:
+// every token of the tile is below V, so no token needs a mask (the masks
+// are 64-bit lane masks per token, and 64 of them do not fit the scalar
+// registers).
+template <bool kFull, int RB>
+__device__ __forceinline__ float2 block_epilogue(const floatx16 (&acc)[4][RB], int rb, int tok0,
+                                                 int V, int half, unsigned char* stage_row) {
+  float x[64];
+#pragma unroll
+  for (int vb = 0; vb < 4; ++vb)
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) {
+      const uint32_t pr = cvt_pk_bf16(acc[vb][rb][r], acc[vb][rb][r + 1]);
+      x[16 * vb + r] = __uint_as_float(pr << 16);
+      x[16 * vb + r + 1] = __uint_as_float(pr & 0xffff0000u);
+    }
+  auto live = [&](int vb, int r) {
+    return kFull || tok0 + 32 * vb + 8 * (r >> 2) + 4 * half + (r & 3) < V;
+  };
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int vb = 0; vb < 4; ++vb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) m = live(vb, r) ? fmaxf(m, x[16 * vb + r]) : m;
+  m = half_max(m);
+  // Tokens at or past V add exactly 0 (z stays a non-negative sum).
+  const float mc = (m == -__builtin_inff()) ? 0.0f : m;
+  float z = 0.0f;
+#pragma unroll
+  for (int vb = 0; vb < 4; ++vb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float e = sg_exp_nonpos(x[16 * vb + r] - mc);
+      z = z + (live(vb, r) ? e : 0.0f);
+    }
+  z = half_sum(z);
+  // bf16 logits into the staging row (LDS rows of 128 tokens); x is already
+  // bf16, so packing keeps its upper halves.
+  auto pack = [&](int i) {
+    return __builtin_amdgcn_perm(__float_as_uint(x[i + 1]), __float_as_uint(x[i]), 0x07060302u);
+  };
+#pragma unroll
+  for (int vb = 0; vb < 4; ++vb)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<uint2*>(stage_row + 2 * (32 * vb + 8 * q + 4 * half)) =
+          make_uint2(pack(16 * vb + 4 * q), pack(16 * vb + 4 * q + 2));
+  return make_float2(m, z);
+}
+
 // Workgroup b -> (vocabulary tile, row tile): the dispatcher places b on XCD
 // b % 8, and the row tiles of one vocabulary tile take consecutive slots of
 // one XCD.
@@ -361,49 +426,25 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
   const bool tile_live = tok0 < V;
   const int n_tiles = (V + kStatTokens - 1) / kStatTokens;
   unsigned char* stage = smem + wave * 32 * R * kOutPitch;
+  auto epilogue = [&](auto full) {
 #pragma unroll
-  for (int rb = 0; rb < R; ++rb) {
-    const int row_local = 32 * rb + col;          // row inside this wave's 32*R rows
-    const int row = r0 + 32 * R * wr + row_local;  // projected row
-    float x[64];
-    float m = -__builtin_inff();
-#pragma unroll
-    for (int vb = 0; vb < 4; ++vb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int tok = tok0 + 32 * vb + 8 * (r >> 2) + 4 * half + (r & 3);
-        x[16 * vb + r] = bf16_to_f32(f32_to_bf16(acc[vb][rb][r]));
-        m = (tok < V) ? fmaxf(m, x[16 * vb + r]) : m;
+    for (int rb = 0; rb < R; ++rb) {
+      const int row_local = 32 * rb + col;          // row inside this wave's 32*R rows
+      const int row = r0 + 32 * R * wr + row_local;  // projected row
+      const float2 mz = block_epilogue<decltype(full)::value>(acc, rb, tok0, V, half,
+                                                              stage + row_local * kOutPitch);
+      if (half == 0 && tile_live && row < a.num_rows) {
+        float* dst =
+            a.tile_stats_dev + (static_cast<int64_t>(row) * n_tiles + tok0 / kStatTokens) * 2;
+        *reinterpret_cast<float2*>(dst) = mz;
       }
-    m = half_max(m);
-    // Tokens at or past V add exactly 0 (z stays a non-negative sum).
-    const float mc = (m == -__builtin_inff()) ? 0.0f : m;
-    float z = 0.0f;
-#pragma unroll
-    for (int vb = 0; vb < 4; ++vb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int tok = tok0 + 32 * vb + 8 * (r >> 2) + 4 * half + (r & 3);
-        const float e = sg_exp_nonpos(x[16 * vb + r] - mc);
-        z = z + ((tok < V) ? e : 0.0f);
-      }
-    z = half_sum(z);  // z_0 + z_1
-    if (half == 0 && tile_live && row < a.num_rows) {
-      float* dst = a.tile_stats_dev + (static_cast<int64_t>(row) * n_tiles + tok0 / kStatTokens) * 2;
-      *reinterpret_cast<float2*>(dst) = make_float2(m, z);
+      __builtin_amdgcn_sched_barrier(0);  // one 32-row block at a time (registers)
     }
-    // bf16 logits into this wave's staging rows (LDS rows of 128 tokens).
-#pragma unroll
-    for (int vb = 0; vb < 4; ++vb)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        uint2 packed;
-        packed.x = pack_bf16x2(x[16 * vb + 4 * q], x[16 * vb + 4 * q + 1]);
-        packed.y = pack_bf16x2(x[16 * vb + 4 * q + 2], x[16 * vb + 4 * q + 3]);
-        *reinterpret_cast<uint2*>(stage + row_local * kOutPitch +
-                                  2 * (32 * vb + 8 * q + 4 * half)) = packed;
-      }
-    __builtin_amdgcn_sched_barrier(0);  // one 32-row block at a time (registers)
+  };
+  if (tok0 + kStatTokens <= V) {
+    epilogue(std::true_type{});
+  } else {
+    epilogue(std::false_type{});
   }
   __builtin_amdgcn_wave_barrier();
   // Row-contiguous read-back: every instruction moves four 256-byte row
@@ -628,48 +669,25 @@ __global__ __launch_bounds__(kPpThreads, 1) void lm_head_pp_kernel(SgLmHeadArgs 
     const bool tile_live = tok0 < V;
     const int n_tiles = (V + kStatTokens - 1) / kStatTokens;
     unsigned char* stage = smem + wave * 64 * kOutPitch;
+    auto epilogue = [&](auto full) {
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      const int row_local = 32 * rb + col;
-      const int row = r0 + 64 * wr + row_local;
-      float x[64];
-      float m = -__builtin_inff();
-#pragma unroll
-      for (int vb = 0; vb < 4; ++vb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int tok = tok0 + 32 * vb + 8 * (r >> 2) + 4 * half + (r & 3);
-          x[16 * vb + r] = bf16_to_f32(f32_to_bf16(acc[vb][rb][r]));
-          m = (tok < V) ? fmaxf(m, x[16 * vb + r]) : m;
+      for (int rb = 0; rb < 2; ++rb) {
+        const int row_local = 32 * rb + col;
+        const int row = r0 + 64 * wr + row_local;
+        const float2 mz = block_epilogue<decltype(full)::value>(acc, rb, tok0, V, half,
+                                                                stage + row_local * kOutPitch);
+        if (half == 0 && tile_live && row < a.num_rows) {
+          float* dst =
+              a.tile_stats_dev + (static_cast<int64_t>(row) * n_tiles + tok0 / kStatTokens) * 2;
+          *reinterpret_cast<float2*>(dst) = mz;
         }
-      m = half_max(m);
-      const float mc = (m == -__builtin_inff()) ? 0.0f : m;
-      float z = 0.0f;
-#pragma unroll
-      for (int vb = 0; vb < 4; ++vb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int tok = tok0 + 32 * vb + 8 * (r >> 2) + 4 * half + (r & 3);
-          const float e = sg_exp_nonpos(x[16 * vb + r] - mc);
-          z = z + ((tok < V) ? e : 0.0f);
-        }
-      z = half_sum(z);
-      if (half == 0 && tile_live && row < a.num_rows) {
-        float* dst =
-            a.tile_stats_dev + (static_cast<int64_t>(row) * n_tiles + tok0 / kStatTokens) * 2;
-        *reinterpret_cast<float2*>(dst) = make_float2(m, z);
+        __builtin_amdgcn_sched_barrier(0);
       }
-#pragma unroll
-      for (int vb = 0; vb < 4; ++vb)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          uint2 packed;
-          packed.x = pack_bf16x2(x[16 * vb + 4 * q], x[16 * vb + 4 * q + 1]);
-          packed.y = pack_bf16x2(x[16 * vb + 4 * q + 2], x[16 * vb + 4 * q + 3]);
-          *reinterpret_cast<uint2*>(stage + row_local * kOutPitch +
-                                    2 * (32 * vb + 8 * q + 4 * half)) = packed;
-        }
-      __builtin_amdgcn_sched_barrier(0);
+    };
+    if (tok0 + kStatTokens <= V) {
+      epilogue(std::true_type{});
+    } else {
+      epilogue(std::false_type{});
     }
     __builtin_amdgcn_wave_barrier();
     if (!tile_live) return;
