@@ -703,11 +703,19 @@ def counters_only(torch, np, W, ops, device, steps, warmup, workload="qwen3_8b")
     """Attention calls (or LM head, decoder layer or tree-sampling calls) plus
     a copy of known size, for rocprofv3 --pmc runs."""
     if workload == "lm_head":
+        # The 752 internal rows: row-major weight, packed weight, and the
+        # library GEMM of the same product (torch.matmul) beside them.
         _, hidden, weight, internal, _ = lm_head_inputs(torch, np, W, device)
         index = torch.from_numpy(internal).to(device)
+        packed = ops.pack_lm_head(weight)
+        sel = hidden[index.long()].contiguous()
         for _ in range(warmup + steps):
             ops.lm_head(hidden, weight, index)
-        torch.cuda.synchronize()
+            torch.cuda.synchronize()
+            ops.lm_head(hidden, packed, index)
+            torch.cuda.synchronize()
+            torch.matmul(sel, weight.T)
+            torch.cuda.synchronize()
         return
     if workload == "layer":
         layer_bench(torch, np, W, ops, device, iters=steps, warmup=warmup)
