@@ -360,7 +360,7 @@ int sg_lm_head_pack_weight(const void* weight_dev, int64_t weight_row_stride, in
 /* sg_lm_head with weight_dev pointing to the packed layout above
  * (weight_row_stride is ignored).  Same outputs, bit for bit; a call of up
  * to 64 rows runs about a fifth faster (every weight copy a contiguous
- * 1 KiB), larger calls about the same. */
+ * 1 KiB), larger calls about 5 % faster. */
 int sg_lm_head_packed(const SgLmHeadArgs* args, sg_stream_t stream);
 
 /* ------------------------------------------------------------------------

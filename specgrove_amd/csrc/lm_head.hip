@@ -579,7 +579,8 @@ __global__ __launch_bounds__(kPpThreads, 1) void lm_head_pp_kernel(SgLmHeadArgs 
   __syncthreads();
 
   // The main loop and the epilogue, once per group (G known at compile time,
-  // so each copy is straight-line code with one product site).  A barrier
+  // so each copy is straight-line code: no branch chooses between product
+  // sites, which would make the compiler copy the accumulators).  A barrier
   // counts arrivals, not instructions: both copies pass 2 steps + 1 barriers.
   // Group A: phase 2t reads stage t and issues stage t+3, phase 2t+1
   // multiplies.  Group B: one idle phase, then phase 2t+1 reads stage t and

@@ -45,7 +45,7 @@ def _check_head(head, hidden, weight, index, oracle, threads=8):
 @pytest.mark.parametrize("rows,hidden,vocab,gather", [
     (1, 64, 1, False), (37, 128, 1000, True), (300, 256, 2049, True),
     (513, 64, 128, False), (256, 192, 255, True), (70, 128, 1153, False),
-    (260, 128, 3000, True)])
+    (260, 128, 3000, True), (129, 256, 700, True), (256, 512, 256, False)])
 def test_lm_head_small_shapes(device, oracle, rows, hidden, vocab, gather):
     print(f"lm_head rows={rows} H={hidden} V={vocab} gather={gather}", flush=True)
     n_hidden = rows * 2 if gather else rows
