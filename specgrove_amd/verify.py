@@ -335,10 +335,16 @@ def tree_verify_hip_lazy_projection_batched(parents_batch: Sequence[Sequence[int
     meta_row_map = meta[n1 + 2 * total:n1 + 3 * total]
     meta_internal = meta[n1 + 3 * total:]
 
-    def projection_valid(head: "ops.LmHeadResult") -> torch.Tensor:
+    def projection_check(head: "ops.LmHeadResult") -> torch.Tensor:
+        """[head status, valid]: the head's status word (0 = every row index
+        in range) always; with ``validate`` also 1 when the statistics are
+        finite with positive sums.  The statistics checks (a few reductions)
+        are skipped without ``validate``, as the reference skips its."""
+        if not validate:
+            return head.status.reshape(1)
         ok = (torch.isfinite(head.row_max).all() & torch.isfinite(head.row_sum).all()
-              & (head.row_sum > 0).all() & (head.status == 0).all())
-        return ok.to(torch.int32).reshape(1)
+              & (head.row_sum > 0).all())
+        return torch.cat([head.status.reshape(1), ok.to(torch.int32).reshape(1)])
 
     if internal_rows.size:
         head = early_head if early_head is not None else ops.lm_head(hidden, weight,
@@ -348,26 +354,29 @@ def tree_verify_hip_lazy_projection_batched(parents_batch: Sequence[Sequence[int
     uniforms, max_depth = _draw_uniforms_beside(topologies, generators, device)
     if internal_rows.size:
         logits, row_max, row_sum = head.logits, head.row_max, head.row_sum
-        valid = projection_valid(head)
+        check = projection_check(head)
     else:  # no tree has an edge: every walk ends at its (unprojected) root
         logits = torch.zeros((1, vocab), dtype=torch.bfloat16, device=device)
         row_max = torch.zeros(1, dtype=torch.float32, device=device)
         row_sum = torch.ones(1, dtype=torch.float32, device=device)
-        valid = torch.ones(1, dtype=torch.int32, device=device)
+        check = torch.tensor([0, 1][:2 if validate else 1], dtype=torch.int32, device=device)
     result = ops.tree_sample_projected(logits, meta_row_offset, meta_parent, meta_token,
                                        uniforms, max_depth, row_max=row_max, row_sum=row_sum,
                                        row_map=meta_row_map)
     # One device-to-host transfer for the walks.
     width = result.accept_nodes.shape[1]
     host = torch.cat([result.accept_len, result.bonus, result.terminal_leaf,
-                      result.accept_nodes.reshape(-1), result.status, valid]).tolist()
+                      result.accept_nodes.reshape(-1), result.status, check]).tolist()
     lengths = host[:count]
     bonuses = host[count:2 * count]
     leaves = host[2 * count:3 * count]
     nodes_flat = host[3 * count:3 * count + count * width]
-    if validate and host[-1] != 1:
+    tail = host[3 * count + count * width:]  # sampler status, head status[, valid]
+    if tail[1] != 0:
+        raise RuntimeError("HIP LM head reported an out-of-range row index")
+    if validate and tail[2] != 1:
         raise FloatingPointError("Invalid batched internal probabilities")
-    if host[-2] != 0:
+    if tail[0] != 0:
         raise RuntimeError("HIP tree sampler returned invalid control values")
 
     leaf_requests = [i for i in range(count) if leaves[i] >= 0]
@@ -393,10 +402,13 @@ def tree_verify_hip_lazy_projection_batched(parents_batch: Sequence[Sequence[int
                                          single_token, leaf_uniforms, 0,
                                          row_max=leaf_head.row_max, row_sum=leaf_head.row_sum)
         leaf_host = torch.cat([leaf.bonus, leaf.accept_len, leaf.status,
-                               projection_valid(leaf_head)]).tolist()
-        if validate and leaf_host[-1] != 1:
+                               projection_check(leaf_head)]).tolist()
+        leaf_tail = leaf_host[2 * m:]  # sampler status, head status[, valid]
+        if leaf_tail[1] != 0:
+            raise RuntimeError("HIP LM head reported an out-of-range row index")
+        if validate and leaf_tail[2] != 1:
             raise FloatingPointError("Invalid lazy-projection leaf probabilities")
-        if leaf_host[-2] != 0 or any(v != 0 for v in leaf_host[m:2 * m]):
+        if leaf_tail[0] != 0 or any(v != 0 for v in leaf_host[m:2 * m]):
             raise RuntimeError("HIP tree sampler returned invalid control values")
         for i, bonus in zip(leaf_requests, leaf_host[:m]):
             bonuses[i] = bonus

@@ -244,3 +244,17 @@ def test_lazy_projection_with_packed_head(device):
                                                             ops.pack_lm_head(weight),
                                                             generators=gens())
     assert [r[:3] for r in plain] == [r[:3] for r in packed]
+
+
+def test_lazy_projection_validate_flag_changes_no_decision(device):
+    """validate=False skips only the statistics checks (finite, positive sums):
+    the decisions and projection counts equal those of validate=True."""
+    sizes = [1, 9, 16, 3, 24, 7]
+    parents, tokens, hidden, weight = _wave(device, 5, sizes)
+    gens = lambda: [torch.Generator(device=device).manual_seed(900 + i)  # noqa: E731
+                    for i in range(len(sizes))]
+    checked = verify.tree_verify_hip_lazy_projection_batched(parents, tokens, hidden, weight,
+                                                             generators=gens(), validate=True)
+    unchecked = verify.tree_verify_hip_lazy_projection_batched(parents, tokens, hidden, weight,
+                                                               generators=gens(), validate=False)
+    assert checked == unchecked
