@@ -23,10 +23,14 @@
 //               its fragment reads for the next stage and its MFMAs are
 //               interleaved in four parts, so that the four waves' LDS
 //               traffic does not queue up right after the barrier;
-//   product   = C^T = W X^T with v_mfma_f32_32x32x16_bf16 (A = weight rows, B =
-//               hidden rows), so each lane ends with 64 logits of one row per
-//               32-row block, fp32-accumulated over the hidden dims in
-//               ascending 16-dim blocks;
+//   product   = C^T = W X^T with v_mfma_f32_16x16x32_bf16 (A = weight rows,
+//               B = hidden rows; one product per 16 x 16 block and 32-dim
+//               stage), so each lane ends with 32 logits of one row per
+//               16-row block (4 consecutive tokens of each 16), fp32-
+//               accumulated over the stages in ascending order (the same
+//               values, bit for bit, as 32x32x16 products over 16-dim
+//               halves gave; the 16x16 shape draws less power, and the GPU
+//               holds a higher clock under it);
 //   epilogue  = round to bf16 (nearest even), per (row, 128-token tile) the
 //               maximum m and z = sum of E(x - m) (the sampler's exp) in the
 //               order below, and the bf16 logits written as whole 256-byte
@@ -58,6 +62,7 @@ namespace {
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(16))) float floatx16;
+typedef __attribute__((ext_vector_type(4))) float floatx4;
 
 constexpr int kLmThreads = 256;
 constexpr int kTileV = 256;          // vocabulary tokens per workgroup tile
@@ -69,7 +74,7 @@ constexpr int kOutPitch = 2 * 128 + 16;  // LDS staging row: 128 bf16 + 16 bytes
 constexpr int kLmXcds = 8;
 constexpr int kMergeRowsPerBlock = 4;   // rows per 256-thread merge workgroup
 
-// Row tile of R 32-row blocks per wave (64*R projected rows per workgroup):
+// Row tile of 32R rows per wave (64R projected rows per workgroup):
 // R = 2 up to 128 rows, 1 up to 64 (the leaf pass), so a small call does not
 // multiply empty rows; R = 4 only where the ping-pong kernel cannot run (a
 // hidden size of 64, two stages).
@@ -131,58 +136,71 @@ __device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
 }
 
-// Epilogue of one 32-row block of a wave's 128-token statistics tile.  The
-// lane's accumulators acc[vb][rb] hold row `col` of the block at tokens
-// tok0 + 32 vb + 8 (r/4) + 4 half + r%4 (element r).  Rounds them to bf16,
-// writes the bf16 logits into the lane's staging row (128 tokens) and
-// returns the tile's (m, z) of the statistics contract: m the maximum, z the
-// sum of E(x - m) in increasing (vb, r) per half, then z_0 + z_1.  kFull:
-// every token of the tile is below V, so no token needs a mask (the masks
-// are 64-bit lane masks per token, and 64 of them do not fit the scalar
-// registers).
-template <bool kFull, int RB>
-__device__ __forceinline__ float2 block_epilogue(const floatx16 (&acc)[4][RB], int rb, int tok0,
-                                                 int V, int half, unsigned char* stage_row) {
-  float x[64];
+// Epilogue of one 16-row block of a wave's 128-token statistics tile.  Lane
+// (g, n) = (lane / 16, lane % 16) holds in acc[tb][rb][i] row n of the block
+// at token tok0 + 16 tb + 4 g + i (the 16x16 MFMA output layout).  Rounds
+// them to bf16, writes the bf16 logits into the lane's staging row (128
+// tokens) and returns the tile's (m, z) of the statistics contract: m the
+// maximum (every lane), z = z_0 + z_1 (lanes g < 2) with z_h the sum of
+// E(x - m) over the half's tokens (bit 2 of the token = h) in increasing
+// token order.  A half's tokens alternate between lanes g = h and g = h + 2
+// in runs of four, so the lower lanes take the upper lanes' values and add
+// them in that order.  kFull: every token of the tile is below V, so no
+// token needs a mask (the masks are 64-bit lane masks per token, and 32 of
+// them do not fit the scalar registers).
+template <bool kFull, int NB>
+__device__ __forceinline__ float2 block_epilogue(const floatx4 (&acc)[8][NB], int rb, int tok0,
+                                                 int V, int g, unsigned char* stage_row) {
+  float x[32];
 #pragma unroll
-  for (int vb = 0; vb < 4; ++vb)
+  for (int tb = 0; tb < 8; ++tb)
 #pragma unroll
-    for (int r = 0; r < 16; r += 2) {
-      const uint32_t pr = cvt_pk_bf16(acc[vb][rb][r], acc[vb][rb][r + 1]);
-      x[16 * vb + r] = __uint_as_float(pr << 16);
-      x[16 * vb + r + 1] = __uint_as_float(pr & 0xffff0000u);
+    for (int i = 0; i < 4; i += 2) {
+      const uint32_t pr = cvt_pk_bf16(acc[tb][rb][i], acc[tb][rb][i + 1]);
+      x[4 * tb + i] = __uint_as_float(pr << 16);
+      x[4 * tb + i + 1] = __uint_as_float(pr & 0xffff0000u);
     }
-  auto live = [&](int vb, int r) {
-    return kFull || tok0 + 32 * vb + 8 * (r >> 2) + 4 * half + (r & 3) < V;
-  };
+  auto live = [&](int tb, int i) { return kFull || tok0 + 16 * tb + 4 * g + i < V; };
   float m = -__builtin_inff();
 #pragma unroll
-  for (int vb = 0; vb < 4; ++vb)
+  for (int tb = 0; tb < 8; ++tb)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) m = live(vb, r) ? fmaxf(m, x[16 * vb + r]) : m;
+    for (int i = 0; i < 4; ++i) m = live(tb, i) ? fmaxf(m, x[4 * tb + i]) : m;
+  m = fmaxf(m, __shfl_xor(m, 16));
   m = half_max(m);
   // Tokens at or past V add exactly 0 (z stays a non-negative sum).
   const float mc = (m == -__builtin_inff()) ? 0.0f : m;
   float z = 0.0f;
 #pragma unroll
-  for (int vb = 0; vb < 4; ++vb)
+  for (int tb = 0; tb < 8; ++tb) {
+    float e[4], pe[4];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float e = sg_exp_nonpos(x[16 * vb + r] - mc);
-      z = z + (live(vb, r) ? e : 0.0f);
+    for (int i = 0; i < 4; ++i) {
+      const float v = sg_exp_nonpos(x[4 * tb + i] - mc);
+      e[i] = live(tb, i) ? v : 0.0f;
     }
-  z = half_sum(z);
+    // Lanes 0..31 receive lanes 32..63's values (the same tokens + 8).
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(e[i]),
+                                                      __float_as_uint(e[i]), false, false);
+      pe[i] = __uint_as_float(r[1]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) z = z + e[i];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) z = z + pe[i];
+  }
+  z = z + __shfl_xor(z, 16);  // z_0 + z_1 in lanes g = 0 and g = 1
   // bf16 logits into the staging row (LDS rows of 128 tokens); x is already
   // bf16, so packing keeps its upper halves.
   auto pack = [&](int i) {
     return __builtin_amdgcn_perm(__float_as_uint(x[i + 1]), __float_as_uint(x[i]), 0x07060302u);
   };
 #pragma unroll
-  for (int vb = 0; vb < 4; ++vb)
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      *reinterpret_cast<uint2*>(stage_row + 2 * (32 * vb + 8 * q + 4 * half)) =
-          make_uint2(pack(16 * vb + 4 * q), pack(16 * vb + 4 * q + 2));
+  for (int tb = 0; tb < 8; ++tb)
+    *reinterpret_cast<uint2*>(stage_row + 2 * (16 * tb + 4 * g)) =
+        make_uint2(pack(4 * tb), pack(4 * tb + 2));
   return make_float2(m, z);
 }
 
@@ -212,8 +230,6 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int half = lane >> 5;
-  const int col = lane & 31;
   const int V = a.vocab;
   const int v0 = vt * kTileV;
   const int r0 = rt * T::kRows;
@@ -282,54 +298,49 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
     for (int i = 0; i < R; ++i) dma16(xk, x_off[i], stage + x_lds[i]);
   };
 
-  floatx16 acc[4][R];
+  // Products: v_mfma_f32_16x16x32_bf16, one per (16-token block, 16-row
+  // block) per stage (all 32 dims of the stage): acc[tb][rb][i] accumulates
+  // token 16 tb + 4 g + i of this wave's 128 and row 16 rb + n of its 32R,
+  // g = lane / 16, n = lane % 16, over the stages in ascending order.
+  constexpr int NB = 2 * R;  // 16-row blocks of this wave
+  floatx4 acc[8][NB];
 #pragma unroll
-  for (int vb = 0; vb < 4; ++vb)
+  for (int tb = 0; tb < 8; ++tb)
 #pragma unroll
-    for (int rb = 0; rb < R; ++rb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[vb][rb][r] = 0.0f;
+    for (int rb = 0; rb < NB; ++rb) acc[tb][rb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
   const int wv = wave & 1;   // vocabulary half of the tile
   const int wr = wave >> 1;  // row half of the tile
-  // Fragment (kb, 32-row block) of lane l: row l%32 of the block, chunk
-  // 2kb + l/32, stored at LDS chunk (2kb + l/32) ^ swz(l%32) of the 64-byte row.
-  int lp[2];
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
-    lp[kb] = (lane & 31) * 64 + 16 * ((2 * kb + (lane >> 5)) ^ (((lane & 31) >> 2) & 3));
-  const int a_base = wv * 4 * 2048;  // first of this wave's 32-row blocks
-  const int b_base = kWBytes + wr * R * 2048;
+  const int g = lane >> 4;
+  // Fragment of a 16-row block for lane l: row l%16 of the block, 16-byte
+  // chunk l/16 (dims 8 (l/16) .. +7 of the stage), stored at LDS chunk
+  // (l/16) ^ swz(l%16) of the 64-byte row.
+  const int lq = (lane & 15) * 64 + 16 * (g ^ (((lane & 15) >> 2) & 3));
+  const int a_base = wv * 8 * 1024;        // this wave's 128 token rows
+  const int b_base = kWBytes + wr * NB * 1024;  // this wave's 32R hidden rows
 
-  // Operand fragments of one stage: weight rows (A) and hidden rows (B) of
-  // both 16-dim blocks, read from LDS one stage ahead of their MFMAs.
+  // Operand fragments of one stage, read from LDS one stage ahead of their
+  // MFMAs.
   struct Frags {
-    bf16x8 w[2][4];
-    bf16x8 x[2][R];
+    bf16x8 a[8];
+    bf16x8 b[NB];
+  };
+  auto frag = [&](const unsigned char* st, int base, int blk) {
+    return as_bf16x8(*reinterpret_cast<const uint4*>(st + base + blk * 1024 + lq));
   };
   auto load_frags = [&](int s, Frags& f) {
     const unsigned char* st = smem + (s % kLmStages) * T::kStage;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int tb = 0; tb < 8; ++tb) f.a[tb] = frag(st, a_base, tb);
 #pragma unroll
-      for (int vb = 0; vb < 4; ++vb)
-        f.w[kb][vb] =
-            as_bf16x8(*reinterpret_cast<const uint4*>(st + a_base + vb * 2048 + lp[kb]));
-#pragma unroll
-      for (int rb = 0; rb < R; ++rb)
-        f.x[kb][rb] =
-            as_bf16x8(*reinterpret_cast<const uint4*>(st + b_base + rb * 2048 + lp[kb]));
-    }
+    for (int rb = 0; rb < NB; ++rb) f.b[rb] = frag(st, b_base, rb);
   };
   auto mma = [&](const Frags& f) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int tb = 0; tb < 8; ++tb)
 #pragma unroll
-      for (int vb = 0; vb < 4; ++vb)
-#pragma unroll
-        for (int rb = 0; rb < R; ++rb)
-          acc[vb][rb] =
-              __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.w[kb][vb], f.x[kb][rb], acc[vb][rb], 0, 0, 0);
+      for (int rb = 0; rb < NB; ++rb)
+        acc[tb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.a[tb], f.b[rb], acc[tb][rb], 0, 0, 0);
   };
   for (int s = 0; s < kLmStages - 1 && s < steps; ++s) issue(s);
   // Stage s: wait for its copies (only the up to two later stages' remain in
@@ -346,7 +357,7 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
     }
     __syncthreads();
   };
-  // Stage s in four parts p (one 32-row weight block each): the MFMAs of
+  // Stage s in four parts p (two 16-token weight blocks each): the MFMAs of
   // stage s-1's dims (fragments `cur`, read during stage s-1), a quarter of
   // the fragment reads of stage s (into `next`) placed one after each of the
   // part's first MFMAs, and a quarter of the copies that refill stage s-1's
@@ -360,39 +371,29 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
     const unsigned char* xk = xbase + static_cast<int64_t>(t) * kStepK * 2;
     const unsigned char* st = smem + (s % kLmStages) * T::kStage;
     constexpr int nd = 4 + R;
+    auto part = [&](auto pc) {
+      constexpr int p = decltype(pc)::value;
+      // Reads: weight blocks 2p, 2p+1 and the hidden blocks j = p (mod 4).
+      constexpr int kReads = 2 + (NB > p ? (NB - p + 3) / 4 : 0);
+      constexpr int kMfmas = 2 * NB;
+      constexpr int kPairs = kReads < kMfmas ? kReads : kMfmas;
+      next.a[2 * p] = frag(st, a_base, 2 * p);
+      next.a[2 * p + 1] = frag(st, a_base, 2 * p + 1);
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
+      for (int j = p; j < NB; j += 4) next.b[j] = frag(st, b_base, j);
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        next.w[kb][p] =
-            as_bf16x8(*reinterpret_cast<const uint4*>(st + a_base + p * 2048 + lp[kb]));
-        if (p < R)
-          next.x[kb][p] =
-              as_bf16x8(*reinterpret_cast<const uint4*>(st + b_base + p * 2048 + lp[kb]));
+      for (int tb = 2 * p; tb < 2 * p + 2; ++tb)
+#pragma unroll
+        for (int rb = 0; rb < NB; ++rb)
+          acc[tb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur.a[tb], cur.b[rb], acc[tb][rb],
+                                                                0, 0, 0);
+#pragma unroll
+      for (int k = 0; k < kPairs; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int rb = 0; rb < R; ++rb)
-          acc[p][rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur.w[kb][p], cur.x[kb][rb],
-                                                               acc[p][rb], 0, 0, 0);
-      if (p < R) {
-        constexpr int kPairs = 4 < 2 * R ? 4 : 2 * R;
-#pragma unroll
-        for (int k = 0; k < kPairs; ++k) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-        if constexpr (2 * R > kPairs) __builtin_amdgcn_sched_group_barrier(0x008, 2 * R - kPairs, 0);
-        if constexpr (4 > kPairs) __builtin_amdgcn_sched_group_barrier(0x100, 4 - kPairs, 0);
-      } else {
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-        if constexpr (2 * R > 2) __builtin_amdgcn_sched_group_barrier(0x008, 2 * R - 2, 0);
-      }
+      if constexpr (kMfmas > kPairs) __builtin_amdgcn_sched_group_barrier(0x008, kMfmas - kPairs, 0);
+      if constexpr (kReads > kPairs) __builtin_amdgcn_sched_group_barrier(0x100, kReads - kPairs, 0);
       if (refill) {
 #pragma unroll
         for (int d = p * nd / 4; d < (p + 1) * nd / 4; ++d) {
@@ -404,7 +405,11 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
         }
       }
       __builtin_amdgcn_sched_barrier(0);
-    }
+    };
+    part(std::integral_constant<int, 0>{});
+    part(std::integral_constant<int, 1>{});
+    part(std::integral_constant<int, 2>{});
+    part(std::integral_constant<int, 3>{});
   };
   Frags f0, f1;
   wait_stage(0);
@@ -420,25 +425,24 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
   mma(f1);
   __syncthreads();  // the ring is free: it becomes the output staging area
 
-  // Epilogue.  acc[vb][rb][r] holds token v0 + 128*wv + 32*vb + 8*(r/4) +
-  // 4*half + r%4 of tile row 32*R*wr + 32*rb + col.
+  // Epilogue, one 16-row block at a time.
   const int tok0 = v0 + 128 * wv;           // first token of this wave's statistics tile
   const bool tile_live = tok0 < V;
   const int n_tiles = (V + kStatTokens - 1) / kStatTokens;
   unsigned char* stage = smem + wave * 32 * R * kOutPitch;
   auto epilogue = [&](auto full) {
 #pragma unroll
-    for (int rb = 0; rb < R; ++rb) {
-      const int row_local = 32 * rb + col;          // row inside this wave's 32*R rows
+    for (int rb = 0; rb < NB; ++rb) {
+      const int row_local = 16 * rb + (lane & 15);   // row inside this wave's 32*R rows
       const int row = r0 + 32 * R * wr + row_local;  // projected row
-      const float2 mz = block_epilogue<decltype(full)::value>(acc, rb, tok0, V, half,
+      const float2 mz = block_epilogue<decltype(full)::value>(acc, rb, tok0, V, g,
                                                               stage + row_local * kOutPitch);
-      if (half == 0 && tile_live && row < a.num_rows) {
+      if (g == 0 && tile_live && row < a.num_rows) {
         float* dst =
             a.tile_stats_dev + (static_cast<int64_t>(row) * n_tiles + tok0 / kStatTokens) * 2;
         *reinterpret_cast<float2*>(dst) = mz;
       }
-      __builtin_amdgcn_sched_barrier(0);  // one 32-row block at a time (registers)
+      __builtin_amdgcn_sched_barrier(0);  // one 16-row block at a time (registers)
     }
   };
   if (tok0 + kStatTokens <= V) {
@@ -474,7 +478,7 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
 // Ping-pong form of the 256-row tile (more than 128 projected rows): eight
 // waves, two per SIMD, in two groups (waves 0-3 and 4-7) half a stage apart.
 // Wave w owns tokens [128*(w&1), +128) and rows [64*(2*(w>>2) + ((w>>1)&1)),
-// +64) of the 256 x 256 tile: 4 x 2 blocks of 32 x 32, 128 accumulators.  In
+// +64) of the 256 x 256 tile: 8 x 4 blocks of 16 x 16, 128 accumulators.  In
 // phase 2t group A (waves 0-3) reads stage t's fragments from LDS and issues
 // its share of the copies of stage t+3 while group B multiplies stage t-1; in
 // phase 2t+1 the groups swap roles.  The two waves of a SIMD thus alternate
@@ -507,8 +511,7 @@ __global__ __launch_bounds__(kPpThreads, 1) void lm_head_pp_kernel(SgLmHeadArgs 
   const int grp = wave >> 2;               // 0: group A, 1: group B
   const int wv = wave & 1;                 // 128-token half of the tile
   const int wr = 2 * grp + ((wave >> 1) & 1);  // 64-row quarter of the tile
-  const int half = lane >> 5;
-  const int col = lane & 31;
+  const int g = lane >> 4;
   const int V = a.vocab;
   const int v0 = vt * kTileV;
   const int r0 = rt * T::kRows;
@@ -558,12 +561,11 @@ __global__ __launch_bounds__(kPpThreads, 1) void lm_head_pp_kernel(SgLmHeadArgs 
     for (int i = 0; i < 2; ++i) dma16(xk, x_off[i], stage + x_lds[i]);
   };
 
-  int lp[2];
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
-    lp[kb] = (lane & 31) * 64 + 16 * ((2 * kb + (lane >> 5)) ^ (((lane & 31) >> 2) & 3));
-  const int a_base = wv * 4 * 2048;
-  const int b_base = kWBytes + wr * 2 * 2048;
+  // Fragments as in lm_head_kernel: lane l reads row l%16 of a 16-row block,
+  // chunk l/16, at LDS chunk (l/16) ^ swz(l%16).
+  const int lq = (lane & 15) * 64 + 16 * (g ^ (((lane & 15) >> 2) & 3));
+  const int a_base = wv * 8 * 1024;      // this wave's 128 token rows
+  const int b_base = kWBytes + wr * 4 * 1024;  // this wave's 64 hidden rows
   // Waits until at most `newer` stages of this wave's copies are in flight.
   auto wait_newer = [&](int newer) {
     if (newer >= 2) {
@@ -589,35 +591,30 @@ __global__ __launch_bounds__(kPpThreads, 1) void lm_head_pp_kernel(SgLmHeadArgs 
   // p+1, so that the barrier publishes the whole stage.
   auto body = [&](auto group) {
     constexpr int G = decltype(group)::value;
-    floatx16 acc[4][2];
+    // acc[tb][rb][i]: token 16 tb + 4 g + i of this wave's 128, row
+    // 16 rb + n of its 64 (lm_head_kernel's products and order).
+    floatx4 acc[8][4];
 #pragma unroll
-    for (int vb = 0; vb < 4; ++vb)
+    for (int tb = 0; tb < 8; ++tb)
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[vb][rb][r] = 0.0f;
-    bf16x8 fw[2][4], fx[2][2];
+      for (int rb = 0; rb < 4; ++rb) acc[tb][rb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    bf16x8 fa[8], fb[4];
     auto read_frags = [&](int t) {
       const unsigned char* st = smem + (t % kLmStages) * T::kStage;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
+      for (int tb = 0; tb < 8; ++tb)
+        fa[tb] = as_bf16x8(*reinterpret_cast<const uint4*>(st + a_base + tb * 1024 + lq));
 #pragma unroll
-        for (int vb = 0; vb < 4; ++vb)
-          fw[kb][vb] = as_bf16x8(*reinterpret_cast<const uint4*>(st + a_base + vb * 2048 + lp[kb]));
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
-          fx[kb][rb] = as_bf16x8(*reinterpret_cast<const uint4*>(st + b_base + rb * 2048 + lp[kb]));
-      }
+      for (int rb = 0; rb < 4; ++rb)
+        fb[rb] = as_bf16x8(*reinterpret_cast<const uint4*>(st + b_base + rb * 1024 + lq));
     };
     auto mma = [&]() {
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int tb = 0; tb < 8; ++tb)
 #pragma unroll
-        for (int vb = 0; vb < 4; ++vb)
-#pragma unroll
-          for (int rb = 0; rb < 2; ++rb)
-            acc[vb][rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fw[kb][vb], fx[kb][rb],
-                                                                  acc[vb][rb], 0, 0, 0);
+        for (int rb = 0; rb < 4; ++rb)
+          acc[tb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[tb], fb[rb], acc[tb][rb], 0, 0,
+                                                                0);
     };
     // One stage: read its fragments (and issue stage t+3 while steps remain),
     // multiply.  N is the number of this wave's stages newer than t+1 that
@@ -664,20 +661,19 @@ __global__ __launch_bounds__(kPpThreads, 1) void lm_head_pp_kernel(SgLmHeadArgs 
     // The ring is free (every barrier above waited for the LDS reads): it
     // becomes the output staging area.
 
-    // Epilogue (lm_head_kernel's, for 2 row blocks): acc[vb][rb][r] holds token
-    // v0 + 128*wv + 32*vb + 8*(r/4) + 4*half + r%4 of tile row 64*wr + 32*rb + col.
+    // Epilogue (lm_head_kernel's, for the wave's four 16-row blocks).
     const int tok0 = v0 + 128 * wv;
     const bool tile_live = tok0 < V;
     const int n_tiles = (V + kStatTokens - 1) / kStatTokens;
     unsigned char* stage = smem + wave * 64 * kOutPitch;
     auto epilogue = [&](auto full) {
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        const int row_local = 32 * rb + col;
+      for (int rb = 0; rb < 4; ++rb) {
+        const int row_local = 16 * rb + (lane & 15);
         const int row = r0 + 64 * wr + row_local;
-        const float2 mz = block_epilogue<decltype(full)::value>(acc, rb, tok0, V, half,
+        const float2 mz = block_epilogue<decltype(full)::value>(acc, rb, tok0, V, g,
                                                                 stage + row_local * kOutPitch);
-        if (half == 0 && tile_live && row < a.num_rows) {
+        if (g == 0 && tile_live && row < a.num_rows) {
           float* dst =
               a.tile_stats_dev + (static_cast<int64_t>(row) * n_tiles + tok0 / kStatTokens) * 2;
           *reinterpret_cast<float2*>(dst) = mz;
