@@ -237,10 +237,11 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
   // DMA slots.  Per stage the weight is 16 copies of 1 KiB (wave w issues
   // 4w .. 4w+3) and the hidden rows 4R (wave w issues Rw .. Rw+R-1).  LDS
   // layout of an operand stage: rows of 64 bytes (the stage's 32 dims) whose
-  // 16-byte chunk c sits at chunk c ^ swz(row), swz(row) = (row >> 2) & 3, so
-  // that each group of 16 lanes of a fragment read (16 consecutive rows, one
-  // chunk each; one 256-byte LDS cycle) touches 16 distinct 16-byte bank
-  // groups.  A copy lane reads 16 contiguous
+  // 16-byte chunk c sits at chunk c ^ swz(row), swz(row) = (row >> 1) & 3:
+  // a fragment read (lane l: row l%16 of a 16-row block, chunk l/16) then
+  // runs without LDS bank conflicts (measured with the bank-conflict counter:
+  // (row >> 2) & 3, row & 3 and no swizzle each cost 4 conflict cycles per
+  // read instruction of this pattern).  A copy lane reads 16 contiguous
   // bytes and four lanes one row's 64 bytes: every copy touches 16 cache
   // lines instead of 32.
   uint32_t w_off[4], w_lds[4], x_off[R], x_lds[R];
@@ -256,7 +257,7 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
   // Copy q moves rows 16q .. 16q+15 of an operand, 64 bytes (the stage's 32
   // dims) of each: lane i reads row 16q + i/4, 16-byte chunk (i%4) ^ swz(row),
   // and lands at LDS chunk i%4 of that row.
-  const int g_lane = (lane & 3) ^ ((lane >> 4) & 3);  // swz(row) = (row >> 2) & 3
+  const int g_lane = (lane & 3) ^ ((lane >> 3) & 3);  // swz(row) = (row >> 1) & 3
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int q = wave * 4 + i;
@@ -314,8 +315,9 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
   const int g = lane >> 4;
   // Fragment of a 16-row block for lane l: row l%16 of the block, 16-byte
   // chunk l/16 (dims 8 (l/16) .. +7 of the stage), stored at LDS chunk
-  // (l/16) ^ swz(l%16) of the 64-byte row.
-  const int lq = (lane & 15) * 64 + 16 * (g ^ (((lane & 15) >> 2) & 3));
+  // (l/16) ^ swz(l%16) of the 64-byte row (16-row blocks start at multiples
+  // of 16 rows, so swz of the block row is swz(l%16)).
+  const int lq = (lane & 15) * 64 + 16 * (g ^ (((lane & 15) >> 1) & 3));
   const int a_base = wv * 8 * 1024;        // this wave's 128 token rows
   const int b_base = kWBytes + wr * NB * 1024;  // this wave's 32R hidden rows
 
@@ -528,7 +530,7 @@ __global__ __launch_bounds__(kPpThreads, 1) void lm_head_pp_kernel(SgLmHeadArgs 
   constexpr int64_t kWStep = kPacked ? kWBytes : kStepK * 2;
   const unsigned char* xbase = static_cast<const unsigned char*>(a.hidden_dev);
   bool bad_index = false;
-  const int g_lane = (lane & 3) ^ ((lane >> 4) & 3);  // swz(row) = (row >> 2) & 3
+  const int g_lane = (lane & 3) ^ ((lane >> 3) & 3);  // swz(row) = (row >> 1) & 3
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int q = 2 * wave + i;
@@ -563,7 +565,7 @@ __global__ __launch_bounds__(kPpThreads, 1) void lm_head_pp_kernel(SgLmHeadArgs 
 
   // Fragments as in lm_head_kernel: lane l reads row l%16 of a 16-row block,
   // chunk l/16, at LDS chunk (l/16) ^ swz(l%16).
-  const int lq = (lane & 15) * 64 + 16 * (g ^ (((lane & 15) >> 2) & 3));
+  const int lq = (lane & 15) * 64 + 16 * (g ^ (((lane & 15) >> 1) & 3));
   const int a_base = wv * 8 * 1024;      // this wave's 128 token rows
   const int b_base = kWBytes + wr * 4 * 1024;  // this wave's 64 hidden rows
   // Waits until at most `newer` stages of this wave's copies are in flight.
