@@ -258,3 +258,25 @@ def test_lazy_projection_validate_flag_changes_no_decision(device):
     unchecked = verify.tree_verify_hip_lazy_projection_batched(parents, tokens, hidden, weight,
                                                                generators=gens(), validate=False)
     assert checked == unchecked
+
+
+@pytest.mark.parametrize("hidden_size", [512, 64])
+def test_lm_head_row_tiles_agree_bit_for_bit(device, hidden_size):
+    """Every kernel gives a row the same logits and statistics bit for bit:
+    the 256-row ping-pong kernel (above 128 rows; the 128-row-per-wave kernel
+    at a hidden size of 64), the 128-row and the 64-row tiles.  The lazy
+    projection projects internal rows and reached leaves in calls of
+    different sizes, so its decisions rely on this."""
+    print(f"lm_head row tiles H={hidden_size}", flush=True)
+    g = torch.Generator(device=device).manual_seed(hidden_size)
+    hidden = torch.randn(400, hidden_size, device=device, generator=g).to(torch.bfloat16)
+    weight = (torch.randn(3001, hidden_size, device=device, generator=g) * 0.05).to(torch.bfloat16)
+    rows = torch.randperm(400, device=device, generator=g)[:300].to(torch.int32)
+    big = ops.lm_head(hidden, weight, rows)
+    torch.cuda.synchronize()
+    for n in (100, 40):
+        part = ops.lm_head(hidden, weight, rows[:n].contiguous())
+        torch.cuda.synchronize()
+        assert torch.equal(part.logits, big.logits[:n]), n
+        for name in ("tile_stats", "row_max", "row_sum"):
+            assert torch.equal(getattr(part, name), getattr(big, name)[:n]), (n, name)
