@@ -105,6 +105,27 @@ __device__ __forceinline__ void dma16(const void* gbase, uint32_t voff, uint32_t
                : "s"(lds), "v"(voff), "s"(gbase)
                : "memory", "m0");
 }
+// The same copy with the non-temporal hint: the line is not kept for reuse.
+__device__ __forceinline__ void dma16_nt(const void* gbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt"
+               :
+               : "s"(lds), "v"(voff), "s"(gbase)
+               : "memory", "m0");
+}
+// Weight copies.  Calls of at most 128 rows have one row tile, so every
+// weight byte is read once: with the packed layout (whole 1 KiB copies) they
+// carry the non-temporal hint (64-row leaf pass 256 -> 239 us, 128 rows
+// 319 -> 311 us).  Row-major copies read half of each 128-byte line per
+// stage and need the line kept for the next stage's half (the hint made
+// them 44 % slower); larger calls re-read each weight tile from L2.
+template <int R, bool kPacked>
+__device__ __forceinline__ void dma16_weight(const void* gbase, uint32_t voff, uint32_t lds) {
+  if constexpr (kPacked && R <= 2) {
+    dma16_nt(gbase, voff, lds);
+  } else {
+    dma16(gbase, voff, lds);
+  }
+}
 
 // s_waitcnt immediate: vmcnt <= n, the other counters unconstrained.
 constexpr int vmcnt_encoding(int n) {
@@ -294,7 +315,7 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
     const unsigned char* wk = wbase + static_cast<int64_t>(s) * kWStep;
     const unsigned char* xk = xbase + static_cast<int64_t>(s) * kStepK * 2;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(wk, w_off[i], stage + w_lds[i]);
+    for (int i = 0; i < 4; ++i) dma16_weight<R, kPacked>(wk, w_off[i], stage + w_lds[i]);
 #pragma unroll
     for (int i = 0; i < R; ++i) dma16(xk, x_off[i], stage + x_lds[i]);
   };
@@ -400,7 +421,7 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
 #pragma unroll
         for (int d = p * nd / 4; d < (p + 1) * nd / 4; ++d) {
           if (d < 4) {
-            dma16(wk, w_off[d], stage_t + w_lds[d]);
+            dma16_weight<R, kPacked>(wk, w_off[d], stage_t + w_lds[d]);
           } else {
             dma16(xk, x_off[d - 4], stage_t + x_lds[d - 4]);
           }
