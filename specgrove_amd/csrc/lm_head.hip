@@ -16,6 +16,8 @@
 // for hidden sizes of 64 (one 4-wave workgroup per CU, 1 wave per SIMD):
 //   tile      = 256 vocabulary tokens x 64 R projected rows; wave w owns the
 //               128 x 32 R quarter (tokens 128*(w&1).., rows 32 R (w>>1)..);
+//               the tiles of a last, partial round of workgroups run as
+//               128-token halves (wave w: rows 16 R w ..) when R <= 2;
 //   ring      = four stages of 32 hidden dims: the weight and hidden chunks
 //               move HBM -> LDS with global_load_lds_dwordx4 (no register
 //               staging), 64 contiguous bytes of each row per copy lane
@@ -78,16 +80,31 @@ constexpr int kMergeRowsPerBlock = 4;   // rows per 256-thread merge workgroup
 // R = 2 up to 128 rows, 1 up to 64 (the leaf pass), so a small call does not
 // multiply empty rows; R = 4 only where the ping-pong kernel cannot run (a
 // hidden size of 64, two stages).
-template <int R>
+// kHalf (R = 1, 2): a workgroup takes one 128-token half of a tile and wave
+// w rows 16 R w .. +16 R of the 64 R, for the tiles of the last, partial
+// round of workgroups (each logit and each statistics tile is computed by one
+// wave in the same order, so the results are the same bit for bit).
+template <int R, bool kHalf = false>
 struct RowTile {
+  static constexpr int kTok = kHalf ? kTileV / 2 : kTileV;  // tokens per workgroup
+  static constexpr int kWB = kTok * kStepK * 2;             // weight bytes per stage
+  static constexpr int kWCopies = kTok / 64;                // weight copies per wave per stage
   static constexpr int kRows = 64 * R;
-  static constexpr int kXBytes = kRows * kStepK * 2;   // hidden bytes per stage
-  static constexpr int kStage = kWBytes + kXBytes;
-  static constexpr int kDmas = 4 + R;                  // copies per wave per stage
-  static constexpr int kStaging = 4 * 32 * R * kOutPitch;
+  static constexpr int kWaveRows = kHalf ? 16 * R : 32 * R;  // projected rows per wave
+  static constexpr int kNB = kWaveRows / 16;                // 16-row blocks per wave
+  static constexpr int kXBytes = kRows * kStepK * 2;        // hidden bytes per stage
+  static constexpr int kStage = kWB + kXBytes;
+  static constexpr int kDmas = kWCopies + R;                // copies per wave per stage
+  static constexpr int kStaging = 4 * kWaveRows * kOutPitch;
   static constexpr int kLds = kLmStages * kStage > kStaging ? kLmStages * kStage : kStaging;
   static constexpr int kBlocksPerCU = R == 1 ? 2 : 1;
 };
+static_assert(RowTile<1, true>::kLds <= RowTile<1>::kLds &&
+                  RowTile<2, true>::kLds <= RowTile<2>::kLds,
+              "half tiles share the kernel's LDS");
+// Workgroup slots of one round (256 CUs): tiles beyond the last whole round
+// run as half tiles.
+constexpr int kRoundCUs = 256;
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return static_cast<uint32_t>(
@@ -241,22 +258,25 @@ __device__ __forceinline__ bool tile_of(int b, int v_tiles, int r_tiles, int& vt
 // contiguous and every copy a contiguous 1 KiB.  Otherwise the weight is
 // row-major [V, weight_row_stride] and a copy reads 64 bytes of each of 16
 // rows.  The arithmetic is the same, so are the results.
-template <int R, bool kPacked>
-__global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_kernel(
-    SgLmHeadArgs a, int v_tiles, int r_tiles) {
-  using T = RowTile<R>;
-  __shared__ __align__(1024) unsigned char smem[T::kLds];
-  int vt, rt;
-  if (!tile_of(blockIdx.x, v_tiles, r_tiles, vt, rt)) return;
+// One workgroup's tile: vocabulary tile vt (its 128-token half `half` when
+// kHalf), row tile rt.
+template <int R, bool kPacked, bool kHalf>
+__device__ __forceinline__ void lm_tile(const SgLmHeadArgs& a, unsigned char* smem, int vt, int rt,
+                                        int half) {
+  using T = RowTile<R, kHalf>;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int V = a.vocab;
-  const int v0 = vt * kTileV;
+  const int v0 = vt * kTileV + T::kTok * half;
   const int r0 = rt * T::kRows;
+  // The second half of the last tile can lie wholly past the vocabulary: no
+  // token, no copy (its weight offsets would start before the tile).
+  if (kHalf && v0 >= V) return;
 
-  // DMA slots.  Per stage the weight is 16 copies of 1 KiB (wave w issues
-  // 4w .. 4w+3) and the hidden rows 4R (wave w issues Rw .. Rw+R-1).  LDS
+  // DMA slots.  Per stage the weight is 4 kWCopies copies of 1 KiB (wave w
+  // issues kWCopies w .. +kWCopies-1: 16 for a whole tile, 8 for a half) and
+  // the hidden rows 4R (wave w issues Rw .. Rw+R-1).  LDS
   // layout of an operand stage: rows of 64 bytes (the stage's 32 dims) whose
   // 16-byte chunk c sits at chunk c ^ swz(row), swz(row) = (row >> 1) & 3:
   // a fragment read (lane l: row l%16 of a 16-row block, chunk l/16) then
@@ -265,11 +285,12 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
   // read instruction of this pattern).  A copy lane reads 16 contiguous
   // bytes and four lanes one row's 64 bytes: every copy touches 16 cache
   // lines instead of 32.
-  uint32_t w_off[4], w_lds[4], x_off[R], x_lds[R];
+  constexpr int kWc = T::kWCopies;
+  uint32_t w_off[kWc], w_lds[kWc], x_off[R], x_lds[R];
   const int steps = a.hidden_size / kStepK;
   const unsigned char* wbase =
       static_cast<const unsigned char*>(a.weight_dev) +
-      (kPacked ? static_cast<int64_t>(vt) * steps * kWBytes
+      (kPacked ? static_cast<int64_t>(vt) * steps * kWBytes + T::kTok * kStepK * 2 * half
                : static_cast<int64_t>(v0) * a.weight_row_stride * 2);
   // Bytes between a tile's consecutive stages.
   constexpr int64_t kWStep = kPacked ? kWBytes : kStepK * 2;
@@ -280,8 +301,8 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
   // and lands at LDS chunk i%4 of that row.
   const int g_lane = (lane & 3) ^ ((lane >> 3) & 3);  // swz(row) = (row >> 1) & 3
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int q = wave * 4 + i;
+  for (int i = 0; i < kWc; ++i) {
+    const int q = wave * kWc + i;
     const int row = 16 * q + (lane >> 2);
     const int dim = 8 * g_lane;
     // Tokens past the vocabulary re-read the last token (finite data the
@@ -305,7 +326,7 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
       src = 0;
     }
     x_off[i] = static_cast<uint32_t>((static_cast<int64_t>(src) * a.hidden_row_stride + dim) * 2);
-    x_lds[i] = static_cast<uint32_t>(kWBytes + 1024 * q);
+    x_lds[i] = static_cast<uint32_t>(T::kWB + 1024 * q);
   }
   if (bad_index && a.status_dev != nullptr) atomicExch(a.status_dev, SG_EINVAL);
 
@@ -315,24 +336,25 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
     const unsigned char* wk = wbase + static_cast<int64_t>(s) * kWStep;
     const unsigned char* xk = xbase + static_cast<int64_t>(s) * kStepK * 2;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma16_weight<R, kPacked>(wk, w_off[i], stage + w_lds[i]);
+    for (int i = 0; i < kWc; ++i) dma16_weight<R, kPacked>(wk, w_off[i], stage + w_lds[i]);
 #pragma unroll
     for (int i = 0; i < R; ++i) dma16(xk, x_off[i], stage + x_lds[i]);
   };
 
   // Products: v_mfma_f32_16x16x32_bf16, one per (16-token block, 16-row
   // block) per stage (all 32 dims of the stage): acc[tb][rb][i] accumulates
-  // token 16 tb + 4 g + i of this wave's 128 and row 16 rb + n of its 32R,
-  // g = lane / 16, n = lane % 16, over the stages in ascending order.
-  constexpr int NB = 2 * R;  // 16-row blocks of this wave
+  // token 16 tb + 4 g + i of this wave's 128 and row 16 rb + n of its
+  // kWaveRows, g = lane / 16, n = lane % 16, over the stages in ascending
+  // order.
+  constexpr int NB = T::kNB;  // 16-row blocks of this wave
   floatx4 acc[8][NB];
 #pragma unroll
   for (int tb = 0; tb < 8; ++tb)
 #pragma unroll
     for (int rb = 0; rb < NB; ++rb) acc[tb][rb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  const int wv = wave & 1;   // vocabulary half of the tile
-  const int wr = wave >> 1;  // row half of the tile
+  const int wv = kHalf ? 0 : wave & 1;      // 128-token half of the tile
+  const int wr = kHalf ? wave : wave >> 1;  // this wave's rows: kWaveRows wr ..
   const int g = lane >> 4;
   // Fragment of a 16-row block for lane l: row l%16 of the block, 16-byte
   // chunk l/16 (dims 8 (l/16) .. +7 of the stage), stored at LDS chunk
@@ -340,7 +362,7 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
   // of 16 rows, so swz of the block row is swz(l%16)).
   const int lq = (lane & 15) * 64 + 16 * (g ^ (((lane & 15) >> 1) & 3));
   const int a_base = wv * 8 * 1024;        // this wave's 128 token rows
-  const int b_base = kWBytes + wr * NB * 1024;  // this wave's 32R hidden rows
+  const int b_base = T::kWB + wr * NB * 1024;  // this wave's hidden rows
 
   // Operand fragments of one stage, read from LDS one stage ahead of their
   // MFMAs.
@@ -393,7 +415,7 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
     const unsigned char* wk = wbase + static_cast<int64_t>(t) * kWStep;
     const unsigned char* xk = xbase + static_cast<int64_t>(t) * kStepK * 2;
     const unsigned char* st = smem + (s % kLmStages) * T::kStage;
-    constexpr int nd = 4 + R;
+    constexpr int nd = kWc + R;
     auto part = [&](auto pc) {
       constexpr int p = decltype(pc)::value;
       // Reads: weight blocks 2p, 2p+1 and the hidden blocks j = p (mod 4).
@@ -420,10 +442,10 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
       if (refill) {
 #pragma unroll
         for (int d = p * nd / 4; d < (p + 1) * nd / 4; ++d) {
-          if (d < 4) {
+          if (d < kWc) {
             dma16_weight<R, kPacked>(wk, w_off[d], stage_t + w_lds[d]);
           } else {
-            dma16(xk, x_off[d - 4], stage_t + x_lds[d - 4]);
+            dma16(xk, x_off[d - kWc], stage_t + x_lds[d - kWc]);
           }
         }
       }
@@ -452,12 +474,12 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
   const int tok0 = v0 + 128 * wv;           // first token of this wave's statistics tile
   const bool tile_live = tok0 < V;
   const int n_tiles = (V + kStatTokens - 1) / kStatTokens;
-  unsigned char* stage = smem + wave * 32 * R * kOutPitch;
+  unsigned char* stage = smem + wave * T::kWaveRows * kOutPitch;
   auto epilogue = [&](auto full) {
 #pragma unroll
     for (int rb = 0; rb < NB; ++rb) {
-      const int row_local = 16 * rb + (lane & 15);   // row inside this wave's 32*R rows
-      const int row = r0 + 32 * R * wr + row_local;  // projected row
+      const int row_local = 16 * rb + (lane & 15);          // row inside this wave's rows
+      const int row = r0 + T::kWaveRows * wr + row_local;  // projected row
       const float2 mz = block_epilogue<decltype(full)::value>(acc, rb, tok0, V, g,
                                                               stage + row_local * kOutPitch);
       if (g == 0 && tile_live && row < a.num_rows) {
@@ -479,9 +501,9 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
   if (!tile_live) return;
   uint16_t* out = static_cast<uint16_t*>(a.logits_dev);
 #pragma unroll 4
-  for (int i = 0; i < 8 * R; ++i) {
+  for (int i = 0; i < T::kWaveRows / 4; ++i) {
     const int row_local = 4 * i + (lane >> 4);
-    const int row = r0 + 32 * R * wr + row_local;
+    const int row = r0 + T::kWaveRows * wr + row_local;
     const int chunk = lane & 15;
     const int tok = tok0 + 8 * chunk;
     const uint4 v = *reinterpret_cast<const uint4*>(stage + row_local * kOutPitch + 16 * chunk);
@@ -496,6 +518,29 @@ __global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_
       }
     }
   }
+}
+
+// The 64- and 128-row kernels (R = 1, 2; one row tile) take the vocabulary
+// tiles of every whole round of workgroups (256 CUs x kBlocksPerCU) as whole
+// tiles (workgroup b: tile b) and split the tiles of the last, partial round
+// into halves (workgroup full_blocks + 2k + h: half h of tile full_blocks +
+// k), which would otherwise run one workgroup to a CU at the end of the
+// launch (82 tiles of Qwen3-8B's 594 cost ~54 us of a 257 us leaf pass).
+// full_blocks: every workgroup when no tile is split.
+template <int R, bool kPacked>
+__global__ __launch_bounds__(kLmThreads, RowTile<R>::kBlocksPerCU) void lm_head_kernel(
+    SgLmHeadArgs a, int v_tiles, int r_tiles, int full_blocks) {
+  __shared__ __align__(1024) unsigned char smem[RowTile<R>::kLds];
+  if constexpr (R <= 2) {
+    const int k = static_cast<int>(blockIdx.x) - full_blocks;
+    if (k >= 0) {
+      lm_tile<R, kPacked, true>(a, smem, full_blocks + k / 2, 0, k & 1);
+      return;
+    }
+  }
+  int vt, rt;
+  if (!tile_of(blockIdx.x, v_tiles, r_tiles, vt, rt)) return;
+  lm_tile<R, kPacked, false>(a, smem, vt, rt, 0);
 }
 
 // Ping-pong form of the 256-row tile (more than 128 projected rows): eight
@@ -817,15 +862,22 @@ int launch_lm_head(const SgLmHeadArgs& a, bool packed, hipStream_t s) {
   auto launch = [&](auto tag) -> int {
     constexpr int R = decltype(tag)::value;
     const int r_tiles = (a.num_rows + RowTile<R>::kRows - 1) / RowTile<R>::kRows;
-    const int64_t blocks =
-        static_cast<int64_t>((v_tiles + kLmXcds - 1) / kLmXcds) * kLmXcds * r_tiles;
+    int64_t blocks = static_cast<int64_t>((v_tiles + kLmXcds - 1) / kLmXcds) * kLmXcds * r_tiles;
+    int full_blocks = static_cast<int>(std::min<int64_t>(blocks, INT32_MAX));
+    constexpr int kSlots = kRoundCUs * RowTile<R>::kBlocksPerCU;
+    if (R <= 2 && v_tiles > kSlots && v_tiles % kSlots != 0) {
+      // Whole rounds as whole tiles, the last partial round as half tiles
+      // (R <= 2: one row tile, so workgroup b of a whole round is tile b).
+      full_blocks = v_tiles / kSlots * kSlots;
+      blocks = full_blocks + 2 * static_cast<int64_t>(v_tiles - full_blocks);
+    }
     SG_REQUIRE(blocks < INT32_MAX, "wave too large");
     if (packed) {
       lm_head_kernel<R, true><<<dim3(static_cast<unsigned>(blocks)), dim3(kLmThreads), 0, s>>>(
-          a, v_tiles, r_tiles);
+          a, v_tiles, r_tiles, full_blocks);
     } else {
       lm_head_kernel<R, false><<<dim3(static_cast<unsigned>(blocks)), dim3(kLmThreads), 0, s>>>(
-          a, v_tiles, r_tiles);
+          a, v_tiles, r_tiles, full_blocks);
     }
     SG_LAUNCH_CHECK();
     return SG_OK;

@@ -280,3 +280,33 @@ def test_lm_head_row_tiles_agree_bit_for_bit(device, hidden_size):
         assert torch.equal(part.logits, big.logits[:n]), n
         for name in ("tile_stats", "row_max", "row_sum"):
             assert torch.equal(getattr(part, name), getattr(big, name)[:n]), (n, name)
+
+
+@pytest.mark.parametrize("vocab", [131372, 131528])
+def test_lm_head_leaf_half_tiles_agree_bit_for_bit(device, oracle, vocab):
+    """The 64- and 128-row kernels run the vocabulary tiles of their last,
+    partial round of workgroups (above 512 and 256 tiles) as 128-token
+    halves.  At 514 tiles (these two vocabularies) tiles 512 and 513 are
+    split; the last half holds no token at 131,372 and 72 at 131,528.  The
+    halves give the rows the same logits and statistics, bit for bit, as the
+    200-row call (whole tiles), with the row-major and the packed weight."""
+    print(f"lm_head leaf half tiles V={vocab}", flush=True)
+    g = torch.Generator(device=device).manual_seed(vocab)
+    hidden = torch.randn(256, 64, device=device, generator=g).to(torch.bfloat16)
+    weight = (torch.randn(vocab, 64, device=device, generator=g) * 0.05).to(torch.bfloat16)
+    rows = torch.randperm(256, device=device, generator=g)[:200].to(torch.int32)
+    packed = ops.pack_lm_head(weight)
+    for w in (weight, packed):
+        big = ops.lm_head(hidden, w, rows)  # 200 rows at H = 64: the four-wave 256-row kernel
+        torch.cuda.synchronize()
+        assert big.status.item() == 0
+        for n in (90, 60):  # the 128-row and the 64-row kernels, with half tiles
+            part = ops.lm_head(hidden, w, rows[:n].contiguous())
+            torch.cuda.synchronize()
+            assert part.status.item() == 0
+            assert torch.equal(part.logits, big.logits[:n]), n
+            for name in ("tile_stats", "row_max", "row_sum"):
+                assert torch.equal(getattr(part, name), getattr(big, name)[:n]), (n, name)
+        # and the 64-row call is the fp32 product within bf16 rounding, with
+        # the oracle's statistics of its logits
+        _check_head(part, hidden, weight, rows[:60], oracle)
