@@ -98,7 +98,10 @@ typedef struct SgTreeAttnArgs {
   int32_t* status_dev;   /* optional [1] device word, never cleared by the library: set
                             to SG_EINVAL when a unit's key range or rows disagree with
                             prefix_len_dev / row_offset_dev (a plan of another wave); that
-                            unit reads no K/V and writes NaN to its output rows */
+                            unit reads no K/V and writes NaN to its output rows.  A unit or
+                            merge group naming a request, kv head or partial slot this
+                            call does not have (a larger wave's plan passed without
+                            plan_host) indexes nothing and only sets the word */
 } SgTreeAttnArgs;
 
 /* Host-side planner.  From host copies of row_offset [n+1] and prefix_len [n]

@@ -236,6 +236,16 @@ struct WaveState {
   floatx16 acc[D / 32];
 };
 
+// The unit's request, kv head and partial slot exist in this call (checked
+// before any of them indexes memory).
+template <int D>
+__device__ __forceinline__ bool unit_indices_valid(const SgTreeAttnArgs& a, const AttnUnit& u) {
+  return u.req >= 0 && u.req < a.num_requests && u.kv_head >= 0 &&
+         u.kv_head < a.num_kv_heads &&
+         (u.partial < 0 ||
+          static_cast<size_t>(u.partial) < a.workspace_bytes / (sizeof(float) * partial_floats(D)));
+}
+
 // The unit's rows and key range lie inside request req's rows and cached
 // prefix as the metadata of this call gives them, and the unit that covers
 // the tree rows ends the key range exactly at the prefix length.
@@ -315,6 +325,13 @@ __device__ __forceinline__ void attn_unit(const SgTreeAttnArgs& a, const AttnUni
   const int r_local = m / G;                    // query row inside the tile
   const int head = u.kv_head * G + (m - r_local * G);
   const bool q_valid = active && r_local < u.row_count;
+  // A record whose request, kv head or partial slot this call does not have
+  // (a plan of a larger wave, or not a plan) indexes nothing: it only marks
+  // the status word.
+  if (!unit_indices_valid<D>(a, u)) {
+    if (tid == 0 && a.status_dev != nullptr) *a.status_dev = SG_EINVAL;
+    return;
+  }
   const int r0 = a.row_offset_dev[u.req];
   const int n = a.row_offset_dev[u.req + 1] - r0;
   // A unit of a plan built for another wave (other prefix lengths or rows)
@@ -865,6 +882,15 @@ __global__ __launch_bounds__(kMergeThreads) void tree_attn_merge_kernel(
   const int sub = blockIdx.x % merge_blocks_per_group(D);
   const MergeGroup grp = groups[blockIdx.x / merge_blocks_per_group(D)];
   const int G = a.num_q_heads / a.num_kv_heads;
+  // A record this call cannot hold (another wave's plan) indexes nothing.
+  const size_t slots = a.workspace_bytes / (sizeof(float) * partial_floats(D));
+  if (grp.req < 0 || grp.req >= a.num_requests || grp.kv_head < 0 ||
+      grp.kv_head >= a.num_kv_heads || grp.row_count < 0 || grp.row_count * G > kQPerUnit ||
+      grp.first_partial < 0 || grp.num_partials < 1 ||
+      static_cast<size_t>(grp.first_partial) + grp.num_partials > slots) {
+    if (threadIdx.x == 0 && a.status_dev != nullptr) *a.status_dev = SG_EINVAL;
+    return;
+  }
   const int r0 = a.row_offset_dev[grp.req];
   const float* ws = static_cast<const float*>(a.workspace_dev);
   const int vectors = grp.row_count * G;

@@ -256,3 +256,38 @@ def test_plan_of_another_wave_is_caught_on_the_device(device, oracle):
     with pytest.raises(ValueError, match="another wave"):
         ops.tree_attention(q[:-1], kc, vc, kt[:-1], vt[:-1], meta["row_offset"],
                            meta["prefix_start"], meta["prefix_len"], meta["parent"], good)
+
+
+def test_plan_of_a_larger_wave_without_host_copy_indexes_nothing(device):
+    """Through the C ABI with no host copy of the plan, a plan built for a
+    larger wave (12 requests against the call's 4; split, so it has merge
+    groups) meets no host check: every unit and merge group whose request,
+    kv head or partial slot the call does not have indexes nothing and only
+    raises the status word, with the plan's own workspace and with one too
+    small for its partials.  The same call with its own plan is then clean."""
+    wl = W.tiny_attention_workload(seed=5, num_q_heads=8, num_kv_heads=2, head_dim=128)
+    _, dev, meta = _inputs(wl, device, 16)
+    big_wl = W.tiny_attention_workload(seed=9, num_requests=12, prefix_lo=600, prefix_hi=900,
+                                       num_q_heads=8, num_kv_heads=2, head_dim=128)
+    big = ops.plan_attention(big_wl.row_offset, big_wl.prefix_len, 8, 2, 128, 4096).to(device)
+    assert big.merges > 0 and big.num_requests == 12
+    good = ops.plan_attention(wl.row_offset, wl.prefix_len, 8, 2, 128).to(device)
+    q, kc, vc, kt, vt = dev
+    small_ws = torch.zeros(16, dtype=torch.uint8, device=device)
+    for ws in (big.workspace, small_ws):
+        print(f"larger-wave plan, workspace {ws.numel()} bytes", flush=True)
+        status = torch.zeros(1, dtype=torch.int32, device=device)
+        call = ops.prepare_tree_attention(q, kc, vc, kt, vt, meta["row_offset"],
+                                          meta["prefix_start"], meta["prefix_len"],
+                                          meta["parent"], good, status=status)
+        call.set(plan_dev=big.device.data_ptr(), plan_host=None, plan_units=big.units,
+                 plan_merges=big.merges, workspace_dev=ws.data_ptr(),
+                 workspace_bytes=ws.numel())
+        call()
+        torch.cuda.synchronize()
+        assert int(status.item()) == ops._lib.SG_EINVAL
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    out = ops.tree_attention(q, kc, vc, kt, vt, meta["row_offset"], meta["prefix_start"],
+                             meta["prefix_len"], meta["parent"], good, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0 and torch.isfinite(out.float()).all()
