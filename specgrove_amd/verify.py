@@ -24,6 +24,7 @@ Differences, by design:
 """
 from __future__ import annotations
 
+import array
 import itertools
 import math
 from typing import Sequence
@@ -210,33 +211,50 @@ def _lazy_hidden(final_hidden: torch.Tensor, count: int, rows: Sequence[int], we
     return hidden if hidden.stride(1) == 1 else hidden.contiguous()
 
 
-def _lazy_meta(parents_batch, tokens_batch):
-    """The lazy walk's packed metadata from the trees' parent and token lists:
-    row_offset [n+1], parent [R], token [R] (-1 at each root), row_map [R]
-    (each node's row among the projected internal rows, else -1), the
-    internal rows' packed indices, and each row's request.  Edges that are not
+def _lazy_rows(parents_batch):
+    """From the trees' parent lists alone: row_offset [n+1], parent [R], each
+    row's request, and the internal rows' packed indices (nodes with a child),
+    which is all the internal-row projection needs.  Edges that are not
     parent < node are skipped, so lists that the topology check would reject
     still give in-range indices; raises TypeError or ValueError when the lists
     do not convert to integers."""
     rows = [len(p) for p in parents_batch]
     count = len(rows)
-    if count < 1 or min(rows) < 1 or len(tokens_batch) != count:
+    if count < 1 or min(rows) < 1:
         raise ValueError("not a batch of trees")
     total = sum(rows)
     row_offset = np.zeros(count + 1, np.int32)
     np.cumsum(rows, out=row_offset[1:])
-    if sum(len(t) for t in tokens_batch) != total - count:
-        raise ValueError("not a batch of trees")
-    # One pass over the Python lists each (int32 range enforced by fromiter).
+    # One pass over the Python lists (int32 range enforced by fromiter).
     parent = np.fromiter(itertools.chain.from_iterable(parents_batch), np.int32, total)
-    token = np.fromiter(itertools.chain.from_iterable(
-        itertools.chain((-1,), t) for t in tokens_batch), np.int32, total)
     owner = np.repeat(np.arange(count, dtype=np.int32), rows)
     local = np.arange(total, dtype=np.int32) - row_offset[owner]
     edge = (parent >= 0) & (parent < local)
     internal = np.zeros(total, bool)
     internal[parent[edge] + row_offset[owner[edge]]] = True
     internal_rows = np.flatnonzero(internal).astype(np.int32)
+    return row_offset, parent, owner, internal_rows
+
+
+def _lazy_meta(parents_batch, tokens_batch, rows=None):
+    """The lazy walk's packed metadata from the trees' parent and token lists:
+    row_offset [n+1], parent [R], token [R] (-1 at each root), row_map [R]
+    (each node's row among the projected internal rows, else -1), the
+    internal rows' packed indices, and each row's request.  ``rows``: the
+    result of _lazy_rows for the same parents, when already computed.  Raises
+    TypeError or ValueError when the lists do not convert to integers."""
+    row_offset, parent, owner, internal_rows = rows if rows is not None else _lazy_rows(
+        parents_batch)
+    count = row_offset.size - 1
+    total = int(row_offset[-1])
+    if len(tokens_batch) != count or sum(len(t) for t in tokens_batch) != total - count:
+        raise ValueError("not a batch of trees")
+    # array.fromlist converts each list in one C loop (int32 range enforced).
+    token = array.array("i")
+    for t in tokens_batch:
+        token.append(-1)
+        token.fromlist(t if isinstance(t, list) else list(t))
+    token = np.frombuffer(token, np.int32)
     row_map = np.full(total, -1, np.int32)
     row_map[internal_rows] = np.arange(internal_rows.size, dtype=np.int32)
     return row_offset, parent, token, row_map, internal_rows, owner
@@ -283,15 +301,22 @@ def tree_verify_hip_lazy_projection_batched(parents_batch: Sequence[Sequence[int
     # every index in range; the kernel also bounds-checks each one); an
     # invalid call then raises below, with the same errors in the same order,
     # before anything is sampled.
+    # Only the internal rows (from the parent lists) come before the launch;
+    # the tokens and the walk's other metadata are built while the GPU
+    # projects, and reach it by a non-blocking copy from pinned memory queued
+    # behind the projection (a pageable copy there would hold the host until
+    # the projection ends).
     early, early_meta, early_head = None, None, None
     try:
         early_hidden = _lazy_hidden(final_hidden, count, [len(p) for p in parents_batch], weight)
         if early_hidden is not None:
-            early = _lazy_meta(parents_batch, tokens_batch)
-            early_meta = torch.from_numpy(np.concatenate(early[:5])).to(early_hidden.device)
-            if early[4].size:
-                n1, tot = count + 1, early[1].size
-                early_head = ops.lm_head(early_hidden, weight, early_meta[n1 + 3 * tot:])
+            early_rows = _lazy_rows(parents_batch)
+            if early_rows[3].size:
+                early_head = ops.lm_head(early_hidden, weight,
+                                         torch.from_numpy(early_rows[3]).to(early_hidden.device))
+            early = _lazy_meta(parents_batch, tokens_batch, early_rows)
+            early_meta = torch.from_numpy(np.concatenate(early[:5])).pin_memory().to(
+                early_hidden.device, non_blocking=True)
     except (TypeError, ValueError, OverflowError):
         early, early_meta, early_head = None, None, None  # the checks below raise
     topologies = [_topology(p, t) for p, t in zip(parents_batch, tokens_batch)]
