@@ -212,12 +212,12 @@ def _lazy_hidden(final_hidden: torch.Tensor, count: int, rows: Sequence[int], we
 
 
 def _lazy_rows(parents_batch):
-    """From the trees' parent lists alone: row_offset [n+1], parent [R], each
-    row's request, and the internal rows' packed indices (nodes with a child),
-    which is all the internal-row projection needs.  Edges that are not
-    parent < node are skipped, so lists that the topology check would reject
-    still give in-range indices; raises TypeError or ValueError when the lists
-    do not convert to integers."""
+    """From the trees' parent lists alone: row_offset [n+1], parent [R] and
+    the internal rows' packed indices (nodes with a child), which is all the
+    internal-row projection needs.  Edges that are not parent < node are
+    skipped, so lists that the topology check would reject still give
+    in-range indices; raises TypeError or ValueError when the lists do not
+    convert to integers."""
     rows = [len(p) for p in parents_batch]
     count = len(rows)
     if count < 1 or min(rows) < 1:
@@ -227,13 +227,11 @@ def _lazy_rows(parents_batch):
     np.cumsum(rows, out=row_offset[1:])
     # One pass over the Python lists (int32 range enforced by fromiter).
     parent = np.fromiter(itertools.chain.from_iterable(parents_batch), np.int32, total)
-    owner = np.repeat(np.arange(count, dtype=np.int32), rows)
-    local = np.arange(total, dtype=np.int32) - row_offset[owner]
-    edge = (parent >= 0) & (parent < local)
+    gpar = parent + np.repeat(row_offset[:-1], rows)  # packed index of each parent
+    edge = (parent >= 0) & (gpar < np.arange(total, dtype=np.int32))
     internal = np.zeros(total, bool)
-    internal[parent[edge] + row_offset[owner[edge]]] = True
-    internal_rows = np.flatnonzero(internal).astype(np.int32)
-    return row_offset, parent, owner, internal_rows
+    internal[gpar[edge]] = True
+    return row_offset, parent, np.flatnonzero(internal).astype(np.int32)
 
 
 def _lazy_meta(parents_batch, tokens_batch, rows=None):
@@ -243,10 +241,10 @@ def _lazy_meta(parents_batch, tokens_batch, rows=None):
     internal rows' packed indices, and each row's request.  ``rows``: the
     result of _lazy_rows for the same parents, when already computed.  Raises
     TypeError or ValueError when the lists do not convert to integers."""
-    row_offset, parent, owner, internal_rows = rows if rows is not None else _lazy_rows(
-        parents_batch)
+    row_offset, parent, internal_rows = rows if rows is not None else _lazy_rows(parents_batch)
     count = row_offset.size - 1
     total = int(row_offset[-1])
+    owner = np.repeat(np.arange(count, dtype=np.int32), np.diff(row_offset))
     if len(tokens_batch) != count or sum(len(t) for t in tokens_batch) != total - count:
         raise ValueError("not a batch of trees")
     # array.fromlist converts each list in one C loop (int32 range enforced).
@@ -311,9 +309,9 @@ def tree_verify_hip_lazy_projection_batched(parents_batch: Sequence[Sequence[int
         early_hidden = _lazy_hidden(final_hidden, count, [len(p) for p in parents_batch], weight)
         if early_hidden is not None:
             early_rows = _lazy_rows(parents_batch)
-            if early_rows[3].size:
+            if early_rows[2].size:
                 early_head = ops.lm_head(early_hidden, weight,
-                                         torch.from_numpy(early_rows[3]).to(early_hidden.device))
+                                         torch.from_numpy(early_rows[2]).to(early_hidden.device))
             early = _lazy_meta(parents_batch, tokens_batch, early_rows)
             early_meta = torch.from_numpy(np.concatenate(early[:5])).pin_memory().to(
                 early_hidden.device, non_blocking=True)
