@@ -82,10 +82,11 @@ def parse_args():
                         "calibrate FETCH_SIZE / WRITE_SIZE; prints nothing")
     p.add_argument("--counters-workload", default="qwen3_8b",
                    choices=["qwen3_8b", "qwen3_4b", "tier128", "long_context", "lm_head",
-                            "layer", "sampler"],
+                            "lm_head_leaf", "layer", "sampler"],
                    help="what a --counters-only run repeats: an attention wave, the LM "
-                        "head over the Qwen3-8B wave's internal rows, one decoder layer, "
-                        "or the 64 x 32 x 151936 tree-sampling call")
+                        "head over the Qwen3-8B wave's internal rows or its 64 leaf rows "
+                        "(the leaf pass), one decoder layer, or the 64 x 32 x 151936 "
+                        "tree-sampling call")
     return p.parse_args()
 
 
@@ -715,6 +716,18 @@ def counters_only(torch, np, W, ops, device, steps, warmup, workload="qwen3_8b")
             ops.lm_head(hidden, packed, index)
             torch.cuda.synchronize()
             torch.matmul(sel, weight.T)
+            torch.cuda.synchronize()
+        return
+    if workload == "lm_head_leaf":
+        # The leaf pass: one leaf row per request (64 rows), row-major weight
+        # and packed weight, each call followed by a synchronisation.
+        _, hidden, weight, _, leaves = lm_head_inputs(torch, np, W, device)
+        index = torch.from_numpy(leaves).to(device)
+        packed = ops.pack_lm_head(weight)
+        for _ in range(warmup + steps):
+            ops.lm_head(hidden, weight, index)
+            torch.cuda.synchronize()
+            ops.lm_head(hidden, packed, index)
             torch.cuda.synchronize()
         return
     if workload == "layer":

@@ -793,9 +793,20 @@ __global__ __launch_bounds__(kMergeRowsPerBlock * kWave) void lm_head_rows_kerne
   const float2* tiles =
       reinterpret_cast<const float2*>(a.tile_stats_dev) + static_cast<int64_t>(row) * n_tiles;
   MZ acc = {-__builtin_inff(), 0.0f};
-  for (int t = lane; t < n_tiles; t += kWave) {
-    const float2 p = tiles[t];
-    acc = merge_mz(acc, MZ{p.x, p.y});
+  // The pairs are loaded 24 at a time before they are merged (the same
+  // merges in the same order): up to 1,536 tiles (196,608 tokens) a row
+  // costs one memory round trip instead of one per merge.
+  constexpr int kBatch = 24;
+  for (int t0 = lane; t0 < n_tiles; t0 += kWave * kBatch) {
+    float2 p[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int t = t0 + kWave * j;
+      p[j] = t < n_tiles ? tiles[t] : make_float2(0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j)
+      if (t0 + kWave * j < n_tiles) acc = merge_mz(acc, MZ{p[j].x, p[j].y});
   }
 #pragma unroll
   for (int d = 32; d >= 1; d >>= 1) {
